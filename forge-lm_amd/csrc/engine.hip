@@ -1,0 +1,907 @@
+// engine.hip -- session engine and C ABI of libforge_hip.so (include/forge_hip.h).
+//
+// A session owns, in device memory:
+//   * the parameters in registry order (GptModel.cs:38-99), each 256-byte
+//     aligned; matrices in the session dtype, vectors always fp32;
+//   * the KV cache, K and V each [L][B][H][ctx][hd] (contiguous 256-byte rows
+//     per head and position, so decode attention streams one head at a time);
+//   * the token history [B][prompt_len + max_new], the step counter, sampler
+//     scratch and activations for B*ctx rows.
+// The token loop (Sampler.Generate, src/LLM.Core/Inference/Sampler.cs:78-109)
+// runs on the stream with no host round trip per token: each step's kernels
+// read the step counter from device memory, the sampler appends the sampled id
+// to the device history and advances the counter.  The host only decides,
+// from the lengths alone, which steps are cached decode steps and which are
+// re-prefills after the window slid (Sampler.cs:93-94 restarts positions at 0,
+// so no cache survives a slide).  Each kind of step is captured once into a
+// HIP graph and replayed.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/forge_hip.h"
+#include "decode_fast.hpp"
+#include "kernels.hpp"
+
+namespace fh {
+void init_registry_random(int seed, int n_layers, const std::vector<int64_t>& offsets,
+                          const std::vector<int64_t>& sizes, const std::vector<int>& kinds, float* w);
+void random_doubles(int seed, int n, double* out);
+}
+
+using namespace fh;
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+static thread_local std::string g_err;
+
+static int set_err(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                                   \
+  do {                                                                                                  \
+    hipError_t e_ = (expr);                                                                             \
+    if (e_ != hipSuccess)                                                                               \
+      return set_err(e_ == hipErrorOutOfMemory ? FH_ERR_OOM : FH_ERR_HIP, "%s failed: %s (%s:%d)", #expr, \
+                     hipGetErrorString(e_), __FILE__, __LINE__);                                        \
+  } while (0)
+
+#define FH_TRY(expr)        \
+  do {                      \
+    int r_ = (expr);        \
+    if (r_ != FH_OK) return r_; \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// registry
+// ---------------------------------------------------------------------------
+namespace {
+
+struct Slot {
+  std::string name;
+  int64_t numel;
+  bool matrix;  // stored in the session dtype
+  int init_kind;  // 0 zero, 1 ones, 2 N(0,0.02), 3 N(0,0.02/sqrt(2L))
+};
+
+std::vector<Slot> make_registry(const fh_model_desc& d) {
+  const int64_t D = d.d_model;
+  std::vector<Slot> r;
+  r.push_back({"tok_emb", (int64_t)d.vocab_size * D, true, 2});
+  r.push_back({"pos_emb", (int64_t)d.context_length * D, true, 2});
+  for (int i = 0; i < d.n_layers; i++) {
+    std::string p = "blocks." + std::to_string(i) + ".";
+    r.push_back({p + "ln1.w", D, false, 1});
+    r.push_back({p + "ln1.b", D, false, 0});
+    r.push_back({p + "attn.qkv.w", D * 3 * D, true, 2});
+    r.push_back({p + "attn.qkv.b", 3 * D, false, 0});
+    r.push_back({p + "attn.proj.w", D * D, true, 3});
+    r.push_back({p + "attn.proj.b", D, false, 0});
+    r.push_back({p + "ln2.w", D, false, 1});
+    r.push_back({p + "ln2.b", D, false, 0});
+    r.push_back({p + "mlp.fc.w", D * 4 * D, true, 2});
+    r.push_back({p + "mlp.fc.b", 4 * D, false, 0});
+    r.push_back({p + "mlp.proj.w", 4 * D * D, true, 3});
+    r.push_back({p + "mlp.proj.b", D, false, 0});
+  }
+  r.push_back({"ln_f.w", D, false, 1});
+  r.push_back({"ln_f.b", D, false, 0});
+  return r;
+}
+
+int validate_desc(const fh_model_desc* d) {
+  if (!d) return set_err(FH_ERR_INVALID, "model descriptor is null");
+  if (d->vocab_size <= 0) return set_err(FH_ERR_INVALID, "VocabSize must be positive.");
+  if (d->context_length <= 0) return set_err(FH_ERR_INVALID, "ContextLength must be positive.");
+  if (d->d_model <= 0) return set_err(FH_ERR_INVALID, "DModel must be positive.");
+  if (d->n_layers <= 0) return set_err(FH_ERR_INVALID, "NLayers must be positive.");
+  if (d->n_heads <= 0) return set_err(FH_ERR_INVALID, "NHeads must be positive.");
+  if (d->d_model % d->n_heads != 0)
+    return set_err(FH_ERR_INVALID, "DModel (%d) must be divisible by NHeads (%d).", d->d_model, d->n_heads);
+  if (d->max_batch <= 0) return set_err(FH_ERR_INVALID, "max_batch must be positive.");
+  if (d->dtype != FH_DTYPE_F32 && d->dtype != FH_DTYPE_BF16) return set_err(FH_ERR_INVALID, "unknown dtype %d", d->dtype);
+  if (d->d_model % 8 != 0 || d->d_model > 1024)
+    return set_err(FH_ERR_UNSUPPORTED, "this build runs DModel in multiples of 8 up to 1024 (got %d)", d->d_model);
+  if (d->d_model / d->n_heads > 128) return set_err(FH_ERR_UNSUPPORTED, "head_dim above 128 is not supported");
+  if (d->vocab_size > 65536) return set_err(FH_ERR_UNSUPPORTED, "vocabularies above 65536 are not supported");
+  return FH_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+struct fh_context {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+  // scratch for fh_sample_logits
+  float* s_work = nullptr;
+  int* s_ints = nullptr;  // tokens | step | done | out | count
+  int s_V = 0, s_hist = 0;
+  double* s_u = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+// session
+// ---------------------------------------------------------------------------
+struct GraphKey {
+  int kind = -1, B = 0, P = 0, max_new = 0, top_k = 0, ngram = 0, eos = 0;
+  float temperature = 0.f, penalty = 0.f;
+  const void* dump = nullptr;
+  const void* uniforms = nullptr;
+  uint64_t gen = 0;
+  bool operator==(const GraphKey& o) const {
+    return kind == o.kind && B == o.B && P == o.P && max_new == o.max_new && top_k == o.top_k && ngram == o.ngram &&
+           eos == o.eos && temperature == o.temperature && penalty == o.penalty && dump == o.dump &&
+           uniforms == o.uniforms && gen == o.gen;
+  }
+};
+
+struct CachedGraph {
+  GraphKey key;
+  hipGraphExec_t exec = nullptr;
+};
+
+struct fh_session {
+  fh_context* ctx = nullptr;
+  fh_model_desc d{};
+  std::vector<Slot> reg;
+  std::vector<size_t> off;  // byte offsets in wbuf
+  char* wbuf = nullptr;
+  size_t wbytes = 0;
+  bool loaded = false;
+  int esize = 4;  // bytes per matrix element
+  // KV cache
+  void* kc = nullptr;
+  void* vc = nullptr;
+  size_t kv_layer = 0;  // elements per layer (B*H*ctx*hd)
+  // activations (rows = B*ctx)
+  float *x = nullptr, *x2 = nullptr, *xn = nullptr, *qkv = nullptr, *o = nullptr, *h = nullptr;
+  float *part = nullptr, *apart = nullptr, *logits = nullptr, *work = nullptr;
+  size_t part_floats = 0;
+  int* step = nullptr;
+  int* done = nullptr;
+  int* out_counts = nullptr;
+  // per-call buffers (grow on demand)
+  int* tokens = nullptr;
+  size_t tokens_cap = 0;
+  int* out_ids = nullptr;
+  size_t out_cap = 0;
+  double* uniforms = nullptr;
+  size_t uni_cap = 0;
+  float* dump = nullptr;
+  size_t dump_cap = 0;
+  uint64_t buf_gen = 1;
+  // fast decode path state
+  FastDecode fast;
+  // graphs
+  CachedGraph g_decode, g_reprefill;
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+  double t_prefill = 0, t_decode = 0;
+  int n_cached = 0, n_reprefill = 0;
+
+  template <typename T>
+  const T* w(size_t i) const {
+    return reinterpret_cast<const T*>(wbuf + off[i]);
+  }
+  const float* v(size_t i) const { return reinterpret_cast<const float*>(wbuf + off[i]); }
+  size_t idx_tok() const { return 0; }
+  size_t idx_pos() const { return 1; }
+  size_t idx_blk(int l, int k) const { return 2 + (size_t)l * 12 + k; }  // k: 0 ln1w .. 11 mpb
+  size_t idx_lnf() const { return 2 + (size_t)d.n_layers * 12; }
+  int B() const { return d.max_batch; }
+  int hd() const { return d.d_model / d.n_heads; }
+};
+
+namespace {
+
+template <typename T>
+int dev_alloc(T** p, size_t count) {
+  if (count == 0) count = 1;
+  void* q = nullptr;
+  hipError_t e = hipMalloc(&q, count * sizeof(T));
+  if (e != hipSuccess)
+    return set_err(e == hipErrorOutOfMemory ? FH_ERR_OOM : FH_ERR_HIP, "hipMalloc(%zu bytes): %s", count * sizeof(T),
+                   hipGetErrorString(e));
+  *p = static_cast<T*>(q);
+  return FH_OK;
+}
+
+template <typename T>
+void dev_free(T*& p) {
+  if (p) (void)hipFree((void*)p);
+  p = nullptr;
+}
+
+template <typename T>
+int ensure(T** p, size_t* cap, size_t need, uint64_t* gen) {
+  if (need <= *cap && *p) return FH_OK;
+  dev_free(*p);
+  *cap = 0;
+  FH_TRY(dev_alloc(p, need));
+  *cap = need;
+  ++*gen;
+  return FH_OK;
+}
+
+void drop_graph(CachedGraph& g) {
+  if (g.exec) (void)hipGraphExecDestroy(g.exec);
+  g.exec = nullptr;
+  g.key = GraphKey{};
+}
+
+int check_launch(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FH_OK;
+  if (e == hipErrorInvalidValue) return set_err(FH_ERR_INVALID, "%s: operand shapes rejected by the kernel wrapper", what);
+  return set_err(FH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define LAUNCH(expr) FH_TRY(check_launch((expr), #expr))
+
+// y = epi(x @ W + b) (+ res) for M rows; split-K GEMV when M <= 4.
+template <typename WT>
+int linear(fh_session* s, const float* x, int M, int K, const WT* W, int N, const float* b, int epi, const float* res,
+           float* y) {
+  hipStream_t st = s->ctx->stream;
+  if (M <= 4) {
+    int S = 0;
+    int splits = std::max(1, std::min(64, K / 16));
+    LAUNCH(launch_gemv_splitk<WT>(st, x, M, K, W, N, s->part, splits, &S));
+    LAUNCH(launch_splitk_epilogue(st, s->part, S, M, N, b, epi, res, y));
+  } else {
+    LAUNCH(launch_gemm<WT>(st, x, M, K, W, N, b, epi, res, y));
+  }
+  return FH_OK;
+}
+
+template <typename WT>
+int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T;
+  for (int l = 0; l < s->d.n_layers; l++) {
+    WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+    WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+    LAUNCH(launch_layernorm(st, s->x, M, M, 0, 0, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), s->xn, D, 1e-5f));
+    FH_TRY(linear<WT>(s, s->xn, M, D, s->w<WT>(s->idx_blk(l, 2)), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
+                      s->qkv));
+    LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, T, D, H, C, kc, vc));
+    LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
+    FH_TRY(linear<WT>(s, s->o, M, D, s->w<WT>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
+    LAUNCH(launch_layernorm(st, s->x2, M, M, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
+    FH_TRY(linear<WT>(s, s->xn, M, D, s->w<WT>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+                      s->h));
+    FH_TRY(linear<WT>(s, s->h, M, 4 * D, s->w<WT>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
+                      s->x));
+  }
+  return FH_OK;
+}
+
+template <typename WT>
+int enqueue_layers_decode(fh_session* s, RowSrc src) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length;
+  for (int l = 0; l < s->d.n_layers; l++) {
+    WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+    WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+    LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), s->xn, D, 1e-5f));
+    FH_TRY(linear<WT>(s, s->xn, B, D, s->w<WT>(s->idx_blk(l, 2)), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
+                      s->qkv));
+    LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, 1, D, H, C, kc, vc));
+    LAUNCH(launch_attn_decode<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, 64, s->o));
+    FH_TRY(linear<WT>(s, s->o, B, D, s->w<WT>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
+    LAUNCH(launch_layernorm(st, s->x2, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
+    FH_TRY(linear<WT>(s, s->xn, B, D, s->w<WT>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+                      s->h));
+    FH_TRY(linear<WT>(s, s->h, B, 4 * D, s->w<WT>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
+                      s->x));
+  }
+  return FH_OK;
+}
+
+struct StepPlan {
+  int P = 0, max_new = 0, tok_stride = 0;
+  const fh_sampling* opts = nullptr;
+  bool with_sample = true;
+};
+
+SampleArgs make_sample_args(fh_session* s, const StepPlan& p) {
+  SampleArgs a{};
+  a.logits = s->logits;
+  a.work = s->work;
+  a.tokens = s->tokens;
+  a.step = s->step;
+  a.done = s->done;
+  a.out_ids = s->out_ids;
+  a.out_counts = s->out_counts;
+  a.uniforms = s->uniforms;
+  a.dump = s->dump;
+  a.B = s->B();
+  a.V = s->d.vocab_size;
+  a.tok_stride = p.tok_stride;
+  a.prompt_len = p.P;
+  a.ctx = s->d.context_length;
+  a.max_new = p.max_new;
+  a.temperature = p.opts->temperature;
+  a.penalty = p.opts->repetition_penalty;
+  a.top_k = p.opts->top_k;
+  a.ngram = p.opts->no_repeat_ngram;
+  a.eos = p.opts->eos_id;
+  return a;
+}
+
+// One forward over a window of T rows per sequence (prefill / re-prefill),
+// then the head on the last row and (optionally) the sampler.
+template <typename WT>
+int enqueue_window_step(fh_session* s, int T, const StepPlan& p) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model;
+  RowSrc src{s->tokens, s->step, p.tok_stride, p.P - T, 0, 0};
+  LAUNCH(launch_embed<WT>(st, src, B, T, s->w<WT>(s->idx_tok()), s->w<WT>(s->idx_pos()), D, s->d.vocab_size,
+                          s->d.context_length, s->x));
+  FH_TRY(enqueue_layers_window<WT>(s, T, src));
+  const size_t lf = s->idx_lnf();
+  LAUNCH(launch_layernorm(st, s->x, B, 1, T, T - 1, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
+  LAUNCH(launch_head<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), s->d.vocab_size, s->logits));
+  if (p.with_sample) LAUNCH(launch_sample(st, make_sample_args(s, p)));
+  return FH_OK;
+}
+
+// One cached decode step: the token sampled last step at position P-1+n.
+template <typename WT>
+int enqueue_decode_step(fh_session* s, const StepPlan& p) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model;
+  RowSrc src{s->tokens, s->step, p.tok_stride, p.P - 1, p.P - 1, 1};
+  if (s->fast.enabled) {
+    FH_TRY(s->fast.enqueue(st, src));
+  } else {
+    LAUNCH(launch_embed<WT>(st, src, B, 1, s->w<WT>(s->idx_tok()), s->w<WT>(s->idx_pos()), D, s->d.vocab_size,
+                            s->d.context_length, s->x));
+    FH_TRY(enqueue_layers_decode<WT>(s, src));
+    const size_t lf = s->idx_lnf();
+    LAUNCH(launch_layernorm(st, s->x, B, 1, 1, 0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
+    LAUNCH(launch_head<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), s->d.vocab_size, s->logits));
+  }
+  LAUNCH(launch_sample(st, make_sample_args(s, p)));
+  return FH_OK;
+}
+
+int enqueue_window(fh_session* s, int T, const StepPlan& p) {
+  return s->d.dtype == FH_DTYPE_BF16 ? enqueue_window_step<bf16_t>(s, T, p) : enqueue_window_step<float>(s, T, p);
+}
+int enqueue_decode(fh_session* s, const StepPlan& p) {
+  return s->d.dtype == FH_DTYPE_BF16 ? enqueue_decode_step<bf16_t>(s, p) : enqueue_decode_step<float>(s, p);
+}
+
+// Captures `enqueue` into `g` unless the cached graph already matches `key`.
+template <class F>
+int capture(fh_session* s, CachedGraph& g, const GraphKey& key, F&& enqueue) {
+  if (g.exec && g.key == key) return FH_OK;
+  drop_graph(g);
+  hipStream_t st = s->ctx->stream;
+  HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue();
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(st, &graph);
+  if (rc != FH_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return rc;
+  }
+  if (e != hipSuccess) return set_err(FH_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(&g.exec, graph, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(graph);
+  if (e != hipSuccess) {
+    g.exec = nullptr;
+    return set_err(FH_ERR_HIP, "graph instantiate failed: %s", hipGetErrorString(e));
+  }
+  g.key = key;
+  return FH_OK;
+}
+
+__global__ void k_fill_int(int* p, int n, int v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int reset_step_state(fh_session* s) {
+  hipStream_t st = s->ctx->stream;
+  hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(64), 0, st, s->step, 1, 0);
+  hipLaunchKernelGGL(k_fill_int, dim3(1), dim3(64), 0, st, s->done, 1, 0);
+  hipLaunchKernelGGL(k_fill_int, dim3((s->B() + 255) / 256), dim3(256), 0, st, s->out_counts, s->B(), -1);
+  HIP_TRY(hipGetLastError());
+  return FH_OK;
+}
+
+int upload_weights(fh_session* s, const float* const* tensors) {
+  // Matrices go to the session dtype; vectors stay fp32 (rounded through bf16
+  // in bf16 sessions so every parameter carries bf16 precision).
+  const bool bf = s->d.dtype == FH_DTYPE_BF16;
+  std::vector<char> host;
+  for (size_t i = 0; i < s->reg.size(); i++) {
+    const Slot& sl = s->reg[i];
+    const float* src = tensors[i];
+    if (!src) return set_err(FH_ERR_INVALID, "tensor %zu (%s) is null", i, sl.name.c_str());
+    size_t bytes;
+    const void* p;
+    if (bf && sl.matrix) {
+      host.resize(sl.numel * 2);
+      bf16_t* h = reinterpret_cast<bf16_t*>(host.data());
+      for (int64_t j = 0; j < sl.numel; j++) h[j] = f32_to_bf16(src[j]);
+      bytes = sl.numel * 2;
+      p = host.data();
+    } else if (bf) {
+      host.resize(sl.numel * 4);
+      float* h = reinterpret_cast<float*>(host.data());
+      for (int64_t j = 0; j < sl.numel; j++) h[j] = bf16_to_f32(f32_to_bf16(src[j]));
+      bytes = sl.numel * 4;
+      p = host.data();
+    } else {
+      bytes = sl.numel * 4;
+      p = src;
+    }
+    HIP_TRY(hipMemcpy(s->wbuf + s->off[i], p, bytes, hipMemcpyHostToDevice));
+  }
+  s->loaded = true;
+  drop_graph(s->g_decode);
+  drop_graph(s->g_reprefill);
+  return s->fast.on_weights_loaded();
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int fh_last_error(char* buf, size_t n) {
+  if (!buf || n == 0) return FH_ERR_INVALID;
+  snprintf(buf, n, "%s", g_err.c_str());
+  return FH_OK;
+}
+
+const char* fh_version(void) { return "forge_hip 0.1 gfx950"; }
+
+int fh_random_doubles(int32_t seed, int n, double* out) {
+  if (n < 0 || (n > 0 && !out)) return set_err(FH_ERR_INVALID, "bad output buffer");
+  random_doubles(seed, n, out);
+  return FH_OK;
+}
+
+int fh_context_create(int device, fh_context** out) {
+  if (!out) return set_err(FH_ERR_INVALID, "out is null");
+  *out = nullptr;
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return set_err(FH_ERR_RANGE, "device %d not present (%d devices)", device, n);
+  auto c = std::make_unique<fh_context>();
+  c->device = device;
+  HIP_TRY(hipSetDevice(device));
+  HIP_TRY(hipGetDeviceProperties(&c->props, device));
+  HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+  *out = c.release();
+  return FH_OK;
+}
+
+int fh_context_destroy(fh_context* c) {
+  if (!c) return FH_OK;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  dev_free(c->s_work);
+  dev_free(c->s_ints);
+  dev_free(c->s_u);
+  if (c->stream) (void)hipStreamDestroy(c->stream);
+  delete c;
+  return FH_OK;
+}
+
+int fh_context_info(fh_context* c, char* name, size_t name_len, uint64_t* total_mem, int32_t* cus) {
+  if (!c) return set_err(FH_ERR_INVALID, "context is null");
+  if (name && name_len) snprintf(name, name_len, "%s (%s)", c->props.name, c->props.gcnArchName);
+  if (total_mem) *total_mem = c->props.totalGlobalMem;
+  if (cus) *cus = c->props.multiProcessorCount;
+  return FH_OK;
+}
+
+int fh_buffer_alloc(fh_context* c, size_t bytes, void** out_dev) {
+  if (!c || !out_dev) return set_err(FH_ERR_INVALID, "null argument");
+  *out_dev = nullptr;
+  HIP_TRY(hipSetDevice(c->device));
+  char* p = nullptr;
+  FH_TRY(dev_alloc(&p, bytes));
+  *out_dev = p;
+  return FH_OK;
+}
+
+int fh_buffer_free(fh_context* c, void* dev) {
+  if (!c) return set_err(FH_ERR_INVALID, "context is null");
+  if (!dev) return FH_OK;
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  HIP_TRY(hipFree(dev));
+  return FH_OK;
+}
+
+int fh_buffer_write(fh_context* c, void* dst_dev, const void* src, size_t bytes) {
+  if (!c || !dst_dev || (!src && bytes)) return set_err(FH_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipMemcpyAsync(dst_dev, src, bytes, hipMemcpyHostToDevice, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return FH_OK;
+}
+
+int fh_buffer_read(fh_context* c, void* dst, const void* src_dev, size_t bytes) {
+  if (!c || !src_dev || (!dst && bytes)) return set_err(FH_ERR_INVALID, "null argument");
+  HIP_TRY(hipSetDevice(c->device));
+  HIP_TRY(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return FH_OK;
+}
+
+int64_t fh_param_count(const fh_model_desc* d) {
+  if (validate_desc(d) != FH_OK) return -1;
+  int64_t n = 0;
+  for (auto& s : make_registry(*d)) n += s.numel;
+  return n;
+}
+
+int fh_param_info(const fh_model_desc* d, int index, char* name, size_t name_len, int64_t* numel) {
+  FH_TRY(validate_desc(d));
+  auto reg = make_registry(*d);
+  if (index < 0 || index >= (int)reg.size())
+    return set_err(FH_ERR_RANGE, "parameter index %d outside [0,%zu)", index, reg.size());
+  if (name && name_len) snprintf(name, name_len, "%s", reg[index].name.c_str());
+  if (numel) *numel = reg[index].numel;
+  return (int)reg.size();
+}
+
+int fh_session_destroy(fh_session* s);
+
+int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out) {
+  if (!c || !out) return set_err(FH_ERR_INVALID, "null argument");
+  *out = nullptr;
+  FH_TRY(validate_desc(desc));
+  HIP_TRY(hipSetDevice(c->device));
+  auto s = std::make_unique<fh_session>();
+  s->ctx = c;
+  s->d = *desc;
+  s->reg = make_registry(*desc);
+  s->esize = desc->dtype == FH_DTYPE_BF16 ? 2 : 4;
+  size_t o = 0;
+  for (auto& sl : s->reg) {
+    s->off.push_back(o);
+    o += ((size_t)sl.numel * (sl.matrix ? s->esize : 4) + 255) / 256 * 256;
+  }
+  s->wbytes = o;
+  fh_session* sp = s.get();
+  auto fail = [&](int rc) {
+    fh_session_destroy(s.release());
+    return rc;
+  };
+  int rc;
+  if ((rc = dev_alloc(&sp->wbuf, sp->wbytes)) != FH_OK) return fail(rc);
+  const int B = desc->max_batch, D = desc->d_model, C = desc->context_length, V = desc->vocab_size;
+  const int H = desc->n_heads, hd = D / H;
+  sp->kv_layer = (size_t)B * H * C * hd;
+  const size_t kvb = sp->kv_layer * desc->n_layers * sp->esize;
+  char* kc = nullptr;
+  char* vc = nullptr;
+  if ((rc = dev_alloc(&kc, kvb)) != FH_OK) return fail(rc);
+  sp->kc = kc;
+  if ((rc = dev_alloc(&vc, kvb)) != FH_OK) return fail(rc);
+  sp->vc = vc;
+  const size_t rows = (size_t)B * C;
+  const int maxc = (C + 63) / 64;
+  sp->part_floats = (size_t)64 * 4 * 4 * D;
+  if ((rc = dev_alloc(&sp->x, rows * D)) || (rc = dev_alloc(&sp->x2, rows * D)) || (rc = dev_alloc(&sp->xn, rows * D)) ||
+      (rc = dev_alloc(&sp->qkv, rows * 3 * D)) || (rc = dev_alloc(&sp->o, rows * D)) ||
+      (rc = dev_alloc(&sp->h, rows * 4 * D)) || (rc = dev_alloc(&sp->part, sp->part_floats)) ||
+      (rc = dev_alloc(&sp->apart, (size_t)B * H * maxc * (hd + 2))) || (rc = dev_alloc(&sp->logits, (size_t)B * V)) ||
+      (rc = dev_alloc(&sp->work, (size_t)B * V)) || (rc = dev_alloc(&sp->step, 1)) || (rc = dev_alloc(&sp->done, 1)) ||
+      (rc = dev_alloc(&sp->out_counts, B)))
+    return fail(rc);
+  for (auto& e : sp->ev) {
+    hipError_t he = hipEventCreate(&e);
+    if (he != hipSuccess) return fail(set_err(FH_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(he)));
+  }
+  if ((rc = sp->fast.init(sp->ctx->stream, *desc, c->props.multiProcessorCount)) != FH_OK) return fail(rc);
+  *out = s.release();
+  return FH_OK;
+}
+
+int fh_session_destroy(fh_session* s) {
+  if (!s) return FH_OK;
+  (void)hipSetDevice(s->ctx->device);
+  (void)hipStreamSynchronize(s->ctx->stream);
+  drop_graph(s->g_decode);
+  drop_graph(s->g_reprefill);
+  s->fast.release();
+  for (auto& e : s->ev)
+    if (e) (void)hipEventDestroy(e);
+  dev_free(s->wbuf);
+  char* kc = static_cast<char*>(s->kc);
+  char* vc = static_cast<char*>(s->vc);
+  dev_free(kc);
+  dev_free(vc);
+  dev_free(s->x); dev_free(s->x2); dev_free(s->xn); dev_free(s->qkv); dev_free(s->o); dev_free(s->h);
+  dev_free(s->part); dev_free(s->apart); dev_free(s->logits); dev_free(s->work);
+  dev_free(s->step); dev_free(s->done); dev_free(s->out_counts);
+  dev_free(s->tokens); dev_free(s->out_ids); dev_free(s->uniforms); dev_free(s->dump);
+  delete s;
+  return FH_OK;
+}
+
+int fh_session_init_random(fh_session* s, int32_t seed) {
+  if (!s) return set_err(FH_ERR_INVALID, "session is null");
+  std::vector<int64_t> offs, sizes;
+  std::vector<int> kinds;
+  int64_t tot = 0;
+  for (auto& sl : s->reg) {
+    offs.push_back(tot);
+    sizes.push_back(sl.numel);
+    kinds.push_back(sl.init_kind);
+    tot += sl.numel;
+  }
+  std::vector<float> w((size_t)tot);
+  init_registry_random(seed, s->d.n_layers, offs, sizes, kinds, w.data());
+  std::vector<const float*> ptrs;
+  for (auto o : offs) ptrs.push_back(w.data() + o);
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  return upload_weights(s, ptrs.data());
+}
+
+int fh_session_load_weights(fh_session* s, const float* const* tensors, int n) {
+  if (!s || !tensors) return set_err(FH_ERR_INVALID, "null argument");
+  if (n != (int)s->reg.size())
+    return set_err(FH_ERR_INVALID, "expected %zu registry tensors, got %d", s->reg.size(), n);
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  return upload_weights(s, tensors);
+}
+
+int fh_session_read_param(fh_session* s, int index, float* out, int64_t numel) {
+  if (!s || !out) return set_err(FH_ERR_INVALID, "null argument");
+  if (index < 0 || index >= (int)s->reg.size()) return set_err(FH_ERR_RANGE, "parameter index %d out of range", index);
+  const Slot& sl = s->reg[index];
+  if (numel != sl.numel) return set_err(FH_ERR_INVALID, "%s has %lld elements, not %lld", sl.name.c_str(),
+                                        (long long)sl.numel, (long long)numel);
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  HIP_TRY(hipStreamSynchronize(s->ctx->stream));
+  if (sl.matrix && s->esize == 2) {
+    std::vector<bf16_t> h(sl.numel);
+    HIP_TRY(hipMemcpy(h.data(), s->wbuf + s->off[index], sl.numel * 2, hipMemcpyDeviceToHost));
+    for (int64_t j = 0; j < sl.numel; j++) out[j] = bf16_to_f32(h[j]);
+  } else {
+    HIP_TRY(hipMemcpy(out, s->wbuf + s->off[index], sl.numel * 4, hipMemcpyDeviceToHost));
+  }
+  return FH_OK;
+}
+
+static int validate_ids(const fh_session* s, const int32_t* ids, size_t n) {
+  for (size_t i = 0; i < n; i++)
+    if ((uint32_t)ids[i] >= (uint32_t)s->d.vocab_size)
+      return set_err(FH_ERR_INVALID, "Token id %d out of range [0,%d).", ids[i], s->d.vocab_size);
+  return FH_OK;
+}
+
+int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* logits_out) {
+  if (!s || !ids || !logits_out) return set_err(FH_ERR_INVALID, "null argument");
+  if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
+  if (batch != s->B()) return set_err(FH_ERR_INVALID, "batch %d must equal the session's max_batch %d", batch, s->B());
+  if (T <= 0) return set_err(FH_ERR_INVALID, "Need at least one token.");
+  if (T > s->d.context_length)
+    return set_err(FH_ERR_INVALID, "Sequence length %d exceeds ContextLength %d.", T, s->d.context_length);
+  FH_TRY(validate_ids(s, ids, (size_t)batch * T));
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  hipStream_t st = s->ctx->stream;
+  FH_TRY(ensure(&s->tokens, &s->tokens_cap, (size_t)batch * T, &s->buf_gen));
+  HIP_TRY(hipMemcpyAsync(s->tokens, ids, sizeof(int32_t) * batch * T, hipMemcpyHostToDevice, st));
+  FH_TRY(reset_step_state(s));
+  fh_sampling greedy{0.f, 0, 1.f, 0, -1, 0};
+  StepPlan p;
+  p.P = T;
+  p.max_new = 1;
+  p.tok_stride = T;
+  p.opts = &greedy;
+  p.with_sample = false;
+  FH_TRY(enqueue_window(s, T, p));
+  HIP_TRY(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * batch * s->d.vocab_size, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  return FH_OK;
+}
+
+int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
+                const double* uniforms, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
+  if (!s || !prompts || !opts || !out_ids || !out_counts) return set_err(FH_ERR_INVALID, "null argument");
+  if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
+  // Sampler.Generate validation, Sampler.cs:82-89, 169-175
+  if (P <= 0) return set_err(FH_ERR_INVALID, "Need at least one prompt token.");
+  if (max_new < 0) return set_err(FH_ERR_RANGE, "maxNewTokens must be >= 0");
+  if (opts->eos_id >= s->d.vocab_size)
+    return set_err(FH_ERR_RANGE, "EOS token must be inside the model vocabulary.");
+  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty < 1.f)
+    return set_err(FH_ERR_RANGE, "Repetition penalty must be finite and >= 1.");
+  if (opts->no_repeat_ngram < 0) return set_err(FH_ERR_RANGE, "No-repeat n-gram size must be >= 0.");
+  if (!std::isfinite(opts->temperature)) return set_err(FH_ERR_INVALID, "Temperature must be finite.");
+  if (batch != s->B()) return set_err(FH_ERR_INVALID, "batch %d must equal the session's max_batch %d", batch, s->B());
+  if (opts->temperature > 0.f && !uniforms)
+    return set_err(FH_ERR_INVALID, "sampling with temperature > 0 needs one uniform per step");
+  FH_TRY(validate_ids(s, prompts, (size_t)batch * P));
+  for (int b = 0; b < batch; b++) out_counts[b] = 0;
+  if (max_new == 0) return FH_OK;
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  hipStream_t st = s->ctx->stream;
+  const int B = batch, V = s->d.vocab_size, C = s->d.context_length;
+  const int stride = P + max_new;
+  FH_TRY(ensure(&s->tokens, &s->tokens_cap, (size_t)B * stride, &s->buf_gen));
+  FH_TRY(ensure(&s->out_ids, &s->out_cap, (size_t)B * max_new, &s->buf_gen));
+  if (uniforms) FH_TRY(ensure(&s->uniforms, &s->uni_cap, (size_t)B * max_new, &s->buf_gen));
+  if (logits_dump) FH_TRY(ensure(&s->dump, &s->dump_cap, (size_t)B * max_new * V, &s->buf_gen));
+  for (int b = 0; b < B; b++)
+    HIP_TRY(hipMemcpyAsync(s->tokens + (size_t)b * stride, prompts + (size_t)b * P, sizeof(int32_t) * P,
+                           hipMemcpyHostToDevice, st));
+  if (uniforms)
+    HIP_TRY(hipMemcpyAsync(s->uniforms, uniforms, sizeof(double) * B * max_new, hipMemcpyHostToDevice, st));
+  FH_TRY(reset_step_state(s));
+
+  StepPlan plan;
+  plan.P = P;
+  plan.max_new = max_new;
+  plan.tok_stride = stride;
+  plan.opts = opts;
+  // dump/uniform pointers are baked into the graphs
+  float* saved_dump = s->dump;
+  double* saved_u = s->uniforms;
+  if (!logits_dump) s->dump = nullptr;
+  if (!uniforms) s->uniforms = nullptr;
+  GraphKey key;
+  key.B = B;
+  key.P = P;
+  key.max_new = max_new;
+  key.top_k = opts->top_k;
+  key.ngram = opts->no_repeat_ngram;
+  key.eos = opts->eos_id;
+  key.temperature = opts->temperature;
+  key.penalty = opts->repetition_penalty;
+  key.dump = s->dump;
+  key.uniforms = s->uniforms;
+  key.gen = s->buf_gen;
+
+  int rc = FH_OK;
+  const int T0 = std::min(P, C);
+  // which of steps 1..max_new-1 are cached decode steps (window fits) vs re-prefills
+  int n_dec = 0, n_re = 0;
+  for (int n = 1; n < max_new; n++) (P + n > C ? n_re : n_dec)++;
+  if (n_dec > 0) {
+    GraphKey k = key;
+    k.kind = 0;
+    rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, plan); });
+  }
+  if (rc == FH_OK && n_re > 0) {
+    GraphKey k = key;
+    k.kind = 1;
+    rc = capture(s, s->g_reprefill, k, [&] { return enqueue_window(s, C, plan); });
+  }
+  if (rc == FH_OK) {
+    (void)hipEventRecord(s->ev[0], st);
+    rc = enqueue_window(s, T0, plan);
+    (void)hipEventRecord(s->ev[1], st);
+    for (int n = 1; rc == FH_OK && n < max_new; n++) {
+      hipError_t e = hipGraphLaunch(P + n > C ? s->g_reprefill.exec : s->g_decode.exec, st);
+      if (e != hipSuccess) rc = set_err(FH_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+    }
+    (void)hipEventRecord(s->ev[2], st);
+  }
+  s->dump = saved_dump;
+  s->uniforms = saved_u;
+  if (rc != FH_OK) {
+    (void)hipStreamSynchronize(st);
+    return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(out_ids, s->out_ids, sizeof(int32_t) * B * max_new, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(out_counts, s->out_counts, sizeof(int32_t) * B, hipMemcpyDeviceToHost, st));
+  if (logits_dump)
+    HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * max_new * V, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  for (int b = 0; b < B; b++)
+    if (out_counts[b] < 0) out_counts[b] = max_new;
+  float ms0 = 0, ms1 = 0;
+  (void)hipEventElapsedTime(&ms0, s->ev[0], s->ev[1]);
+  (void)hipEventElapsedTime(&ms1, s->ev[1], s->ev[2]);
+  s->t_prefill = ms0;
+  s->t_decode = ms1;
+  s->n_cached = n_dec;
+  s->n_reprefill = n_re;
+  return FH_OK;
+}
+
+int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t* cached, int32_t* reprefill) {
+  if (!s) return set_err(FH_ERR_INVALID, "session is null");
+  if (prefill_ms) *prefill_ms = s->t_prefill;
+  if (decode_ms) *decode_ms = s->t_decode;
+  if (cached) *cached = s->n_cached;
+  if (reprefill) *reprefill = s->n_reprefill;
+  return FH_OK;
+}
+
+int fh_sample_logits(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                     const fh_sampling* opts, double u01, int32_t* out_id) {
+  if (!c || !logits_dev || !opts || !out_id || (n_hist > 0 && !history))
+    return set_err(FH_ERR_INVALID, "null argument");
+  if (V <= 0 || V > 65536) return set_err(FH_ERR_UNSUPPORTED, "V must be in [1, 65536]");
+  if (n_hist < 0) return set_err(FH_ERR_INVALID, "n_hist must be >= 0");
+  if (!std::isfinite(opts->temperature)) return set_err(FH_ERR_INVALID, "Temperature must be finite.");
+  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty < 1.f)
+    return set_err(FH_ERR_RANGE, "Repetition penalty must be finite and >= 1.");
+  if (opts->no_repeat_ngram < 0) return set_err(FH_ERR_RANGE, "No-repeat n-gram size must be >= 0.");
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  if (V > c->s_V) {
+    dev_free(c->s_work);
+    FH_TRY(dev_alloc(&c->s_work, V));
+    c->s_V = V;
+  }
+  const int need = n_hist + 1 + 4;
+  if (need > c->s_hist) {
+    dev_free(c->s_ints);
+    FH_TRY(dev_alloc(&c->s_ints, need));
+    c->s_hist = need;
+  }
+  if (!c->s_u) FH_TRY(dev_alloc(&c->s_u, 1));
+  int* tokens = c->s_ints;
+  int* misc = c->s_ints + n_hist + 1;  // step, done, out, count
+  if (n_hist > 0) HIP_TRY(hipMemcpyAsync(tokens, history, sizeof(int32_t) * n_hist, hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(c->s_u, &u01, sizeof(double), hipMemcpyHostToDevice, st));
+  const int init[4] = {0, 0, 0, -1};
+  HIP_TRY(hipMemcpyAsync(misc, init, sizeof init, hipMemcpyHostToDevice, st));
+  SampleArgs a{};
+  a.logits = logits_dev;
+  a.work = c->s_work;
+  a.tokens = tokens;
+  a.step = misc;
+  a.done = misc + 1;
+  a.out_ids = misc + 2;
+  a.out_counts = misc + 3;
+  a.uniforms = c->s_u;
+  a.dump = nullptr;
+  a.B = 1;
+  a.V = V;
+  a.tok_stride = n_hist + 1;
+  a.prompt_len = n_hist;
+  a.ctx = n_hist > 0 ? n_hist : 1;
+  a.max_new = 1;
+  a.temperature = opts->temperature;
+  a.penalty = opts->repetition_penalty;
+  a.top_k = opts->top_k;
+  a.ngram = opts->no_repeat_ngram;
+  a.eos = -1;
+  if (n_hist == 0) {
+    // an empty history never triggers the controls (T = 0 < ngram - 1 only for ngram > 1)
+    a.ctx = 1;
+    a.prompt_len = 0;
+  }
+  hipError_t e = launch_sample(st, a);
+  if (e != hipSuccess) return check_launch(e, "launch_sample");
+  int32_t r = 0;
+  HIP_TRY(hipMemcpyAsync(&r, misc + 2, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipStreamSynchronize(st));
+  *out_id = r;
+  return FH_OK;
+}
+
+}  // extern "C"

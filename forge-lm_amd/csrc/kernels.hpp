@@ -1,0 +1,72 @@
+// kernels.hpp -- launch wrappers for the generic gfx950 kernels (kernels.hip).
+// Vectors (LayerNorm weights, biases) are fp32 in every session; matrices are
+// fp32 or bf16 (WT).  Every wrapper checks on the host that its operands fit what the kernel and
+// its grid assume before launching, and returns a hipError_t.
+#pragma once
+
+#include "common.hpp"
+
+namespace fh {
+
+enum Epilogue : int { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2 };
+
+// x[r,:] = tok_emb[id(r)] + pos_emb[pos(r)] for rows r = b*T + t.
+template <typename WT>
+hipError_t launch_embed(hipStream_t st, RowSrc src, int B, int T, const WT* tok, const WT* pos, int d, int V,
+                        int ctx, float* x);
+
+// out[r,:] = LN(in[r_in,:]) with r_in = r_in0 + (r / rows_per_seq) * seq_stride + (r % rows_per_seq).
+hipError_t launch_layernorm(hipStream_t st, const float* in, int rows, int rows_per_seq, int seq_stride,
+                            int r_in0, const float* w, const float* b, float* out, int d, float eps);
+
+// Split-K GEMV for M <= 4 rows: part[s][m][n] = sum_{k in chunk s} x[m,k] W[k,n].
+template <typename WT>
+hipError_t launch_gemv_splitk(hipStream_t st, const float* x, int M, int K, const WT* W, int N, float* part,
+                              int splits, int* used_splits);
+
+// y[m,n] = epi(sum_s part[s][m][n] + bias[n]) (+ res[m,n]).
+hipError_t launch_splitk_epilogue(hipStream_t st, const float* part, int splits, int M, int N, const float* bias,
+                                  int epi, const float* res, float* y);
+
+// Tiled GEMM for any M: y[m,n] = epi(sum_k a[m,k] W[k,n] + bias[n]) (+ res[m,n]).
+template <typename WT>
+hipError_t launch_gemm(hipStream_t st, const float* a, int M, int K, const WT* W, int N, const float* bias, int epi,
+                       const float* res, float* y);
+
+// K/V columns of qkv [B*T, 3d] into the cache [B][H][ctx][hd] at positions pos(row).
+template <typename KT>
+hipError_t launch_kv_store(hipStream_t st, RowSrc src, const float* qkv, int B, int T, int d, int H, int ctx,
+                           KT* kcache, KT* vcache);
+
+// Causal attention of every window row (prefill): o[r, h*hd:] for r = b*T + t over keys 0..t.
+template <typename KT>
+hipError_t launch_attn_prefill(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
+                               const KT* kcache, const KT* vcache, float* o);
+
+// Decode attention of one row per sequence over keys 0..pos (pos from src), split over
+// chunks of `chunk` keys, then combined.  part must hold B*H*max_chunks*(hd+2) floats.
+template <typename KT>
+hipError_t launch_attn_decode(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
+                              const KT* kcache, const KT* vcache, float* part, int chunk, float* o);
+
+// Tied head for B rows: logits[b, v] = dot(xn[b,:], E[v,:]).
+template <typename WT>
+hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* E, int V, float* logits);
+
+struct SampleArgs {
+  const float* logits;  // [B][V] raw ForwardLast logits
+  float* work;          // [B][V] scratch
+  int* tokens;          // [B][tok_stride] prompt + generated ids
+  int* step;            // device step counter (advanced by the last block)
+  int* done;            // block arrival counter (zeroed before first use; self-resetting)
+  int* out_ids;         // [B][max_new]
+  int* out_counts;      // [B]
+  const double* uniforms;  // [B][max_new] or null
+  float* dump;          // [B][max_new][V] or null
+  int B, V, tok_stride, prompt_len, ctx, max_new;
+  float temperature, penalty;
+  int top_k, ngram, eos;
+};
+hipError_t launch_sample(hipStream_t st, const SampleArgs& a);
+
+}  // namespace fh

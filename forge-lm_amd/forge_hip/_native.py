@@ -1,0 +1,113 @@
+"""ctypes binding of libforge_hip.so (include/forge_hip.h).
+
+The library is built in-tree by ``forge-lm_amd/csrc/Makefile`` into
+``forge-lm_amd/build/libforge_hip.so``.  There is no fallback: if the library
+is missing or a GPU call fails, the error is raised.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_ROOT, "build", "libforge_hip.so")
+
+FH_OK = 0
+FH_ERR_INVALID = -1
+FH_ERR_RANGE = -2
+FH_ERR_HIP = -3
+FH_ERR_OOM = -4
+FH_ERR_STATE = -5
+FH_ERR_UNSUPPORTED = -6
+
+FH_DTYPE_F32 = 0
+FH_DTYPE_BF16 = 1
+
+# Every symbol include/forge_hip.h declares (checked by the CPU tests).
+EXPORTS = (
+    "fh_last_error", "fh_version", "fh_random_doubles", "fh_context_create", "fh_context_destroy",
+    "fh_context_info", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
+    "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
+    "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
+    "fh_generate", "fh_last_timing", "fh_sample_logits",
+)
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [("vocab_size", ctypes.c_int32), ("context_length", ctypes.c_int32),
+                ("d_model", ctypes.c_int32), ("n_layers", ctypes.c_int32), ("n_heads", ctypes.c_int32),
+                ("max_batch", ctypes.c_int32), ("dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class Sampling(ctypes.Structure):
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", ctypes.c_int32),
+                ("repetition_penalty", ctypes.c_float), ("no_repeat_ngram", ctypes.c_int32),
+                ("eos_id", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+
+class HipError(RuntimeError):
+    """A libforge_hip call returned a negative status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"{msg} (status {code})")
+        self.code = code
+
+
+class ArgumentError(HipError, ValueError):
+    """FH_ERR_INVALID / FH_ERR_RANGE: the reference's ArgumentException family."""
+
+
+_lib = None
+
+
+def lib():
+    """Loads the library once; raises FileNotFoundError if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i32, i64, f32, f64 = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_double
+    P = ctypes.POINTER
+    L.fh_last_error.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+    L.fh_version.restype = ctypes.c_char_p
+    L.fh_random_doubles.argtypes = [i32, ctypes.c_int, vp]
+    L.fh_context_create.argtypes = [ctypes.c_int, P(vp)]
+    L.fh_context_destroy.argtypes = [vp]
+    L.fh_context_info.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, P(ctypes.c_uint64), P(i32)]
+    L.fh_buffer_alloc.argtypes = [vp, ctypes.c_size_t, P(vp)]
+    L.fh_buffer_free.argtypes = [vp, vp]
+    L.fh_buffer_write.argtypes = [vp, vp, vp, ctypes.c_size_t]
+    L.fh_buffer_read.argtypes = [vp, vp, vp, ctypes.c_size_t]
+    L.fh_session_create.argtypes = [vp, P(ModelDesc), P(vp)]
+    L.fh_session_destroy.argtypes = [vp]
+    L.fh_param_count.argtypes = [P(ModelDesc)]
+    L.fh_param_count.restype = i64
+    L.fh_param_info.argtypes = [P(ModelDesc), ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t, P(i64)]
+    L.fh_session_init_random.argtypes = [vp, i32]
+    L.fh_session_load_weights.argtypes = [vp, P(vp), ctypes.c_int]
+    L.fh_session_read_param.argtypes = [vp, ctypes.c_int, vp, i64]
+    L.fh_forward_last.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]
+    L.fh_generate.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp, vp, vp, vp]
+    L.fh_last_timing.argtypes = [vp, P(f64), P(f64), P(i32), P(i32)]
+    L.fh_sample_logits.argtypes = [vp, vp, ctypes.c_int, vp, ctypes.c_int, P(Sampling), f64, P(i32)]
+    _lib = L
+    return L
+
+
+def last_error() -> str:
+    buf = ctypes.create_string_buffer(1024)
+    lib().fh_last_error(buf, len(buf))
+    return buf.value.decode(errors="replace")
+
+
+def check(code: int) -> int:
+    """Raises on a negative status; returns non-negative values unchanged."""
+    if code >= 0:
+        return code
+    msg = last_error()
+    if code in (FH_ERR_INVALID, FH_ERR_RANGE):
+        raise ArgumentError(code, msg)
+    raise HipError(code, msg)

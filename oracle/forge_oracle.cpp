@@ -1,0 +1,609 @@
+// forge_oracle.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// CPU restatement of the reference ForgeLM inference path, used as the parity
+// checker for the HIP library and as the CPU baseline in bench.py.  Nothing in
+// the product (forge-lm_amd/) links, loads or calls this file; only tests/,
+// __graft_entry__.smoke() and bench.py's cpu_baseline leg do.
+//
+// Every function follows a reference file:line (paths relative to the
+// reference checkout root).  Compile with -ffp-contract=off so every
+// "multiply then add" in the reference stays two roundings.
+//
+// Pinning status of each part (what checks it in tests/):
+//   NetRandom ............ parity unpinned vs .NET (no runtime here); restated
+//                          from the published subtractive generator (Knuth
+//                          TAOCP 3.2.2 / Numerical Recipes ran3).  Weights and
+//                          uniforms are generated once and fed to both this
+//                          oracle and the GPU, so GPU parity does not depend
+//                          on it.  Statistical checks only (mean/var, range).
+//   Pcg32 ................ pinned by the PCG32 reference formula (O'Neill 2014)
+//                          checked in Python against an independent big-int
+//                          restatement plus the unbiased-bound rejection rule.
+//   gelu ................. pinned by CpuBackendTests.Gelu_KnownValues.
+//   layernorm ............ pinned by LayerNorm_NormalizesRows (closed forms).
+//   softmax .............. pinned by Softmax_RowsSumToOne incl. the 1000 case.
+//   matmuls / dot ........ brute force vs float64 naive matmul (1e-4), and the
+//                          exact sequential-k order vs a numpy float32 loop.
+//   dot lane order ....... parity unpinned: Vector<float>.Count=8 and the
+//                          Vector.Sum lane order are .NET JIT details.
+//   sampler .............. pinned by every InferenceTests literal.
+//   forward .............. KV-cached decode == full recompute bit-for-bit,
+//                          ForwardLast == last row of Forward exactly,
+//                          parameter counts 7232 / 97,934,592 / 219,237,376.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <limits>
+#include <thread>
+#include <unordered_set>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// System.Random(seed) legacy seeded generator (Net5CompatSeedImpl).
+// Used by Tensor.FillNormal (src/LLM.Core/Tensor/Tensor.cs:79-91) and by the
+// sampler's single NextDouble per sampled step (Sampler.cs:61).
+// ---------------------------------------------------------------------------
+struct NetRandom {
+    int seed_array[56];
+    int inext = 0, inextp = 21;
+    explicit NetRandom(int seed) {
+        const int MBIG = 2147483647, MSEED = 161803398;
+        int subtraction = (seed == INT32_MIN) ? MBIG : std::abs(seed);
+        int mj = MSEED - subtraction;
+        seed_array[55] = mj;
+        int mk = 1, ii = 0;
+        for (int i = 1; i < 55; i++) {
+            ii += 21;
+            if (ii >= 55) ii -= 55;
+            seed_array[ii] = mk;
+            mk = mj - mk;
+            if (mk < 0) mk += MBIG;
+            mj = seed_array[ii];
+        }
+        for (int k = 1; k < 5; k++)
+            for (int i = 1; i < 56; i++) {
+                int n = i + 30;
+                if (n >= 55) n -= 55;
+                seed_array[i] -= seed_array[1 + n];
+                if (seed_array[i] < 0) seed_array[i] += MBIG;
+            }
+        seed_array[0] = 0;
+    }
+    int internal_sample() {
+        const int MBIG = 2147483647;
+        int a = inext + 1;
+        if (a >= 56) a = 1;
+        int b = inextp + 1;
+        if (b >= 56) b = 1;
+        int r = seed_array[a] - seed_array[b];
+        if (r == MBIG) r--;
+        if (r < 0) r += MBIG;
+        seed_array[a] = r;
+        inext = a;
+        inextp = b;
+        return r;
+    }
+    double next_double() { return internal_sample() * (1.0 / 2147483647.0); }
+};
+
+// PCG32 as in src/LLM.Core/Training/TrainingRandom.cs:13-72 (prompt ids).
+struct Pcg32 {
+    uint64_t state = 0, inc = 0xDA3E39CB94B95BDBull;
+    explicit Pcg32(int seed) {
+        next_u32();
+        state += (uint64_t)(uint32_t)seed;
+        next_u32();
+    }
+    uint32_t next_u32() {
+        uint64_t old = state;
+        state = old * 6364136223846793005ull + inc;
+        uint32_t xs = (uint32_t)(((old >> 18) ^ old) >> 27);
+        int rot = (int)(old >> 59);
+        return (xs >> rot) | (xs << ((-rot) & 31));
+    }
+    int next(int max_excl) {
+        uint32_t bound = (uint32_t)max_excl;
+        uint32_t threshold = (0u - bound) % bound;
+        for (;;) {
+            uint32_t v = next_u32();
+            if (v >= threshold) return (int)(v % bound);
+        }
+    }
+};
+
+// Tensor.FillNormal, Tensor.cs:79-91: Box-Muller pairs in double.
+void fill_normal(float* data, int64_t n, NetRandom& rng, float std_) {
+    for (int64_t i = 0; i < n; i += 2) {
+        double u1 = 1.0 - rng.next_double();
+        double u2 = rng.next_double();
+        double r = std::sqrt(-2.0 * std::log(u1));
+        data[i] = (float)(r * std::cos(2 * M_PI * u2) * (double)std_);
+        if (i + 1 < n) data[i + 1] = (float)(r * std::sin(2 * M_PI * u2) * (double)std_);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Model configuration and parameter registry (ModelConfig.cs:8-25,
+// GptModel.cs:38-99, ModelPresets.cs:49-58).
+// ---------------------------------------------------------------------------
+struct Cfg {
+    int V, ctx, d, L, H;
+    int hd() const { return d / H; }
+    int hidden() const { return 4 * d; }
+};
+
+struct Layout {  // float offsets of every parameter in registry order
+    int64_t tok, pos;
+    struct Blk { int64_t ln1w, ln1b, qkvw, qkvb, projw, projb, ln2w, ln2b, fcw, fcb, mpw, mpb; };
+    std::vector<Blk> blk;
+    int64_t lnfw, lnfb, total;
+};
+
+Layout make_layout(const Cfg& c) {
+    Layout l;
+    int64_t o = 0, d = c.d;
+    l.tok = o; o += (int64_t)c.V * d;
+    l.pos = o; o += (int64_t)c.ctx * d;
+    for (int i = 0; i < c.L; i++) {
+        Layout::Blk b;
+        b.ln1w = o; o += d;
+        b.ln1b = o; o += d;
+        b.qkvw = o; o += d * 3 * d;
+        b.qkvb = o; o += 3 * d;
+        b.projw = o; o += d * d;
+        b.projb = o; o += d;
+        b.ln2w = o; o += d;
+        b.ln2b = o; o += d;
+        b.fcw = o; o += d * 4 * d;
+        b.fcb = o; o += 4 * d;
+        b.mpw = o; o += 4 * d * d;
+        b.mpb = o; o += d;
+        l.blk.push_back(b);
+    }
+    l.lnfw = o; o += d;
+    l.lnfb = o; o += d;
+    l.total = o;
+    return l;
+}
+
+// ---------------------------------------------------------------------------
+// CpuBackend forward kernels (src/LLM.Core/Tensor/CpuBackend.cs).
+// ---------------------------------------------------------------------------
+constexpr int64_t kSmallMatMulWork = 8000000;  // CpuBackend.cs:29
+int g_threads = 1;                              // Parallel.For width (1 = sequential)
+
+template <class F>
+void parallel_rows(int M, int64_t work, F&& f) {
+    if (work <= kSmallMatMulWork || g_threads <= 1 || M < 2) {
+        for (int m = 0; m < M; m++) f(m);
+        return;
+    }
+    int nt = std::min(g_threads, M);
+    std::atomic<int> next{0};
+    std::vector<std::thread> th;
+    for (int t = 0; t < nt; t++)
+        th.emplace_back([&] {
+            for (int m; (m = next.fetch_add(1)) < M;) f(m);
+        });
+    for (auto& t : th) t.join();
+}
+
+// Vector.Sum over the 8 lanes of a 256-bit Vector<float>.  The lane order is a
+// JIT detail (parity unpinned); this restatement adds the two 128-bit halves
+// and then reduces pairwise.
+inline float vsum8(const float* a) {
+    float h0 = a[0] + a[4], h1 = a[1] + a[5], h2 = a[2] + a[6], h3 = a[3] + a[7];
+    return (h0 + h1) + (h2 + h3);
+}
+
+// CpuBackend.Dot, CpuBackend.cs:197-220: 8 lane partial sums, Vector.Sum, scalar tail.
+float dot_net(const float* x, const float* y, int n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i <= n - 8; i += 8)
+        for (int l = 0; l < 8; l++) acc[l] = acc[l] + x[i + l] * y[i + l];
+    float s = vsum8(acc);
+    for (; i < n; i++) s = s + x[i] * y[i];
+    return s;
+}
+
+// MatMulNN via MatMulRowKernel(Seq), CpuBackend.cs:49-57, 118-164, 175-194:
+// y[m,:] = 0; for k ascending: y[m,:] += a[m,k] * b[k,:]  (mul, then add).
+void matmul_nn(const float* a, const float* b, float* y, int M, int K, int N) {
+    parallel_rows(M, (int64_t)M * K * N, [&](int m) {
+        float* yr = y + (int64_t)m * N;
+        for (int n = 0; n < N; n++) yr[n] = 0.f;
+        for (int k = 0; k < K; k++) {
+            float s = a[(int64_t)m * K + k];
+            const float* br = b + (int64_t)k * N;
+            for (int n = 0; n < N; n++) yr[n] = yr[n] + s * br[n];
+        }
+    });
+}
+
+// MatMulNT, CpuBackend.cs:71-115: y[m,n] = Dot(a[m,:], b[n,:]).
+void matmul_nt(const float* a, const float* b, float* y, int M, int K, int N) {
+    parallel_rows(M, (int64_t)M * K * N, [&](int m) {
+        const float* ar = a + (int64_t)m * K;
+        float* yr = y + (int64_t)m * N;
+        for (int n = 0; n < N; n++) yr[n] = dot_net(ar, b + (int64_t)n * K, K);
+    });
+}
+
+// AddBias, CpuBackend.cs:285-289 (AddInPlace per row).
+void add_bias(float* y, const float* b, int rows, int cols) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++) y[(int64_t)r * cols + c] = y[(int64_t)r * cols + c] + b[c];
+}
+
+// AddInPlace, CpuBackend.cs:311-318.
+void add_in_place(float* dst, const float* src, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dst[i] = dst[i] + src[i];
+}
+
+// LayerNormForward, CpuBackend.cs:377-398 (eps from Layers.cs:100).
+void layernorm(const float* x, const float* w, const float* b, float* out, int rows, int cols, float eps) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (int64_t)r * cols;
+        float* o = out + (int64_t)r * cols;
+        float sum = 0.f;
+        for (int c = 0; c < cols; c++) sum = sum + xr[c];
+        float mu = sum / (float)cols;
+        float var_sum = 0.f;
+        for (int c = 0; c < cols; c++) {
+            float dd = xr[c] - mu;
+            var_sum = var_sum + dd * dd;
+        }
+        float rs = 1.f / std::sqrt(var_sum / (float)cols + eps);
+        for (int c = 0; c < cols; c++) o[c] = (xr[c] - mu) * rs * w[c] + b[c];
+    }
+}
+
+// SoftmaxForward, CpuBackend.cs:446-458.
+void softmax_rows(float* x, int rows, int cols) {
+    for (int r = 0; r < rows; r++) {
+        float* row = x + (int64_t)r * cols;
+        float mx = row[0];
+        for (int c = 1; c < cols; c++) mx = std::fmax(mx, row[c]);
+        float sum = 0.f;
+        for (int c = 0; c < cols; c++) {
+            row[c] = std::exp(row[c] - mx);
+            sum = sum + row[c];
+        }
+        float inv = 1.f / sum;
+        for (int c = 0; c < cols; c++) row[c] = row[c] * inv;
+    }
+}
+
+// Gelu, CpuBackend.cs:25-26, 510-514.
+const float kGeluC = std::sqrt(2.f / 3.14159265f);
+inline float gelu(float v) {
+    float u = kGeluC * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.f + std::tanh(u));
+}
+
+// ---------------------------------------------------------------------------
+// Full-recompute forward over one window (GptModel.ForwardCore,
+// GptModel.cs:212-222, Layers.cs forward methods).  This is the reference
+// algorithm: every row of the window, every step.
+// ---------------------------------------------------------------------------
+void forward_full(const Cfg& c, const Layout& lay, const float* W, const int* ids, int T, float* logits) {
+    const int d = c.d, H = c.H, hd = c.hd(), F = c.hidden();
+    const float inv_scale = 1.f / std::sqrt((float)hd);  // Layers.cs:174
+    std::vector<float> x((int64_t)T * d), pe((int64_t)T * d), h((int64_t)T * d), qkv((int64_t)T * 3 * d);
+    std::vector<float> q((int64_t)T * hd), k((int64_t)T * hd), v((int64_t)T * hd), probs((int64_t)T * T);
+    std::vector<float> ctxv((int64_t)T * hd), concat((int64_t)T * d), a((int64_t)T * d);
+    std::vector<float> f((int64_t)T * F), g((int64_t)T * F), m((int64_t)T * d);
+    // Embedding.Forward x2 + AddInPlace (GptModel.cs:217-218, CpuBackend.cs:527-531)
+    for (int t = 0; t < T; t++) {
+        std::memcpy(&x[(int64_t)t * d], W + lay.tok + (int64_t)ids[t] * d, d * sizeof(float));
+        std::memcpy(&pe[(int64_t)t * d], W + lay.pos + (int64_t)t * d, d * sizeof(float));
+    }
+    add_in_place(x.data(), pe.data(), (int64_t)T * d);
+    for (int l = 0; l < c.L; l++) {
+        const auto& B = lay.blk[l];
+        // TransformerBlock.Forward, Layers.cs:384-392
+        layernorm(x.data(), W + B.ln1w, W + B.ln1b, h.data(), T, d, 1e-5f);
+        matmul_nn(h.data(), W + B.qkvw, qkv.data(), T, d, 3 * d);
+        add_bias(qkv.data(), W + B.qkvb, T, 3 * d);
+        // MultiHeadAttention.Forward, Layers.cs:191-229, one (B=1) slot per head
+        for (int s = 0; s < H; s++) {
+            for (int t = 0; t < T; t++)  // PackQkvHeads default, ITensorBackend.cs:58-65
+                for (int e = 0; e < hd; e++) {
+                    q[(int64_t)t * hd + e] = qkv[(int64_t)t * 3 * d + s * hd + e];
+                    k[(int64_t)t * hd + e] = qkv[(int64_t)t * 3 * d + d + s * hd + e];
+                    v[(int64_t)t * hd + e] = qkv[(int64_t)t * 3 * d + 2 * d + s * hd + e];
+                }
+            matmul_nt(q.data(), k.data(), probs.data(), T, hd, T);  // BatchedMatMulNT
+            // ScaledCausalSoftmaxForward default, ITensorBackend.cs:117-122
+            for (int64_t i = 0; i < (int64_t)T * T; i++) probs[i] = probs[i] * inv_scale;
+            for (int i = 0; i < T; i++)
+                for (int j = i + 1; j < T; j++) probs[(int64_t)i * T + j] = -INFINITY;
+            softmax_rows(probs.data(), T, T);
+            matmul_nn(probs.data(), v.data(), ctxv.data(), T, T, hd);  // BatchedMatMulNN
+            for (int t = 0; t < T; t++)  // UnpackHeads
+                for (int e = 0; e < hd; e++) concat[(int64_t)t * d + s * hd + e] = ctxv[(int64_t)t * hd + e];
+        }
+        matmul_nn(concat.data(), W + B.projw, a.data(), T, d, d);
+        add_bias(a.data(), W + B.projb, T, d);
+        add_in_place(a.data(), x.data(), (int64_t)T * d);  // a += x
+        layernorm(a.data(), W + B.ln2w, W + B.ln2b, h.data(), T, d, 1e-5f);
+        matmul_nn(h.data(), W + B.fcw, f.data(), T, d, F);  // Mlp.Forward, Layers.cs:306-313
+        add_bias(f.data(), W + B.fcb, T, F);
+        for (int64_t i = 0; i < (int64_t)T * F; i++) g[i] = gelu(f[i]);
+        matmul_nn(g.data(), W + B.mpw, m.data(), T, F, d);
+        add_bias(m.data(), W + B.mpb, T, d);
+        add_in_place(m.data(), a.data(), (int64_t)T * d);  // m += a
+        x.swap(m);
+    }
+    layernorm(x.data(), W + lay.lnfw, W + lay.lnfb, h.data(), T, d, 1e-5f);
+    matmul_nt(h.data(), W + lay.tok, logits, T, d, c.V);  // TiedOutputProjection, Layers.cs:80-86
+}
+
+// ---------------------------------------------------------------------------
+// KV-cached restatement: computes only the rows the reference would read (the
+// last row), reusing keys/values of earlier rows.  Because every reference
+// kernel is row-independent and masked probabilities are exactly 0 (0*v adds
+// nothing), this reproduces the full recompute's last row bit-for-bit; tests
+// check that claim directly.
+// ---------------------------------------------------------------------------
+struct Cached {
+    Cfg c;
+    Layout lay;
+    const float* W;
+    std::vector<float> kc, vc;  // [L][H][ctx][hd]
+    int len = 0;                // positions held
+    Cached(const Cfg& cfg, const float* w) : c(cfg), lay(make_layout(cfg)), W(w) {
+        size_t n = (size_t)c.L * c.H * c.ctx * c.hd();
+        kc.assign(n, 0.f);
+        vc.assign(n, 0.f);
+    }
+    // Runs rows [len, len+T) at positions len.. and returns the last row's logits.
+    void rows(const int* ids, int T, float* logits_last) {
+        const int d = c.d, H = c.H, hd = c.hd(), F = c.hidden();
+        const float inv_scale = 1.f / std::sqrt((float)hd);
+        std::vector<float> x((int64_t)T * d), pe((int64_t)T * d), h((int64_t)T * d), qkv((int64_t)T * 3 * d);
+        std::vector<float> concat((int64_t)T * d), a((int64_t)T * d), f((int64_t)T * F), g((int64_t)T * F),
+            m((int64_t)T * d), sc(c.ctx), o(hd);
+        for (int t = 0; t < T; t++) {
+            std::memcpy(&x[(int64_t)t * d], W + lay.tok + (int64_t)ids[t] * d, d * sizeof(float));
+            std::memcpy(&pe[(int64_t)t * d], W + lay.pos + (int64_t)(len + t) * d, d * sizeof(float));
+        }
+        add_in_place(x.data(), pe.data(), (int64_t)T * d);
+        for (int l = 0; l < c.L; l++) {
+            const auto& B = lay.blk[l];
+            layernorm(x.data(), W + B.ln1w, W + B.ln1b, h.data(), T, d, 1e-5f);
+            matmul_nn(h.data(), W + B.qkvw, qkv.data(), T, d, 3 * d);
+            add_bias(qkv.data(), W + B.qkvb, T, 3 * d);
+            for (int s = 0; s < H; s++) {
+                float* K = &kc[(((size_t)l * H + s) * c.ctx) * hd];
+                float* Vv = &vc[(((size_t)l * H + s) * c.ctx) * hd];
+                for (int t = 0; t < T; t++)
+                    for (int e = 0; e < hd; e++) {
+                        K[(size_t)(len + t) * hd + e] = qkv[(int64_t)t * 3 * d + d + s * hd + e];
+                        Vv[(size_t)(len + t) * hd + e] = qkv[(int64_t)t * 3 * d + 2 * d + s * hd + e];
+                    }
+                for (int t = 0; t < T; t++) {
+                    int i = len + t;  // absolute row; attends j <= i
+                    const float* qr = &qkv[(int64_t)t * 3 * d + s * hd];
+                    for (int j = 0; j <= i; j++) sc[j] = dot_net(qr, K + (size_t)j * hd, hd) * inv_scale;
+                    softmax_rows(sc.data(), 1, i + 1);
+                    for (int e = 0; e < hd; e++) o[e] = 0.f;
+                    for (int j = 0; j <= i; j++)
+                        for (int e = 0; e < hd; e++) o[e] = o[e] + sc[j] * Vv[(size_t)j * hd + e];
+                    for (int e = 0; e < hd; e++) concat[(int64_t)t * d + s * hd + e] = o[e];
+                }
+            }
+            matmul_nn(concat.data(), W + B.projw, a.data(), T, d, d);
+            add_bias(a.data(), W + B.projb, T, d);
+            add_in_place(a.data(), x.data(), (int64_t)T * d);
+            layernorm(a.data(), W + B.ln2w, W + B.ln2b, h.data(), T, d, 1e-5f);
+            matmul_nn(h.data(), W + B.fcw, f.data(), T, d, F);
+            add_bias(f.data(), W + B.fcb, T, F);
+            for (int64_t i = 0; i < (int64_t)T * F; i++) g[i] = gelu(f[i]);
+            matmul_nn(g.data(), W + B.mpw, m.data(), T, F, d);
+            add_bias(m.data(), W + B.mpb, T, d);
+            add_in_place(m.data(), a.data(), (int64_t)T * d);
+            x.swap(m);
+        }
+        len += T;
+        layernorm(&x[(int64_t)(T - 1) * d], W + lay.lnfw, W + lay.lnfb, h.data(), 1, d, 1e-5f);
+        matmul_nt(h.data(), W + lay.tok, logits_last, 1, d, c.V);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Sampler (src/LLM.Core/Inference/Sampler.cs).
+// ---------------------------------------------------------------------------
+int greedy(const float* l, int v) {  // Sampler.cs:14-20
+    int best = 0;
+    for (int i = 1; i < v; i++)
+        if (l[i] > l[best]) best = i;
+    return best;
+}
+
+// Sampler.cs:29-69 with the one NextDouble draw passed in as `u01`.
+int sample(const float* logits, int v, float temperature, int top_k, double u01) {
+    if (temperature <= 0.f) return greedy(logits, v);
+    std::vector<float> p(logits, logits + v);
+    for (int i = 0; i < v; i++) p[i] = p[i] / temperature;
+    if (top_k > 0 && top_k < v) {
+        std::vector<float> sorted(p);
+        std::sort(sorted.begin(), sorted.end());
+        float thr = sorted[v - top_k];
+        for (int i = 0; i < v; i++)
+            if (p[i] < thr) p[i] = -INFINITY;
+    }
+    float mx = -INFINITY;
+    for (int i = 0; i < v; i++)
+        if (p[i] > mx) mx = p[i];
+    float sum = 0.f;
+    for (int i = 0; i < v; i++) {
+        p[i] = std::exp(p[i] - mx);
+        sum = sum + p[i];
+    }
+    float u = (float)u01 * sum;
+    float acc = 0.f;
+    for (int i = 0; i < v; i++) {
+        acc = acc + p[i];
+        if (u < acc) return i;
+    }
+    return v - 1;
+}
+
+// Sampler.ApplyRepetitionControls, Sampler.cs:111-165.
+void apply_repetition_controls(float* l, int v, const int* hist, int n, float penalty, int ngram) {
+    if (penalty != 1.f) {
+        std::unordered_set<int> seen;
+        for (int i = 0; i < n; i++) {
+            int t = hist[i];
+            if ((unsigned)t >= (unsigned)v || !seen.insert(t).second) continue;
+            l[t] = l[t] < 0.f ? l[t] * penalty : l[t] / penalty;
+        }
+    }
+    if (ngram <= 0 || n < ngram - 1) return;
+    std::vector<float> before(l, l + v);
+    if (ngram == 1) {
+        for (int i = 0; i < n; i++)
+            if ((unsigned)hist[i] < (unsigned)v) l[hist[i]] = -INFINITY;
+    } else {
+        int pre = ngram - 1, suf = n - pre;
+        for (int s = 0; s + ngram <= n; s++) {
+            bool match = true;
+            for (int j = 0; j < pre; j++)
+                if (hist[s + j] != hist[suf + j]) { match = false; break; }
+            if (!match) continue;
+            int banned = hist[s + pre];
+            if ((unsigned)banned < (unsigned)v) l[banned] = -INFINITY;
+        }
+    }
+    bool any = false;
+    for (int i = 0; i < v; i++)
+        if (!std::isinf(l[i]) || l[i] > 0) { any = true; break; }
+    if (!any) std::memcpy(l, before.data(), sizeof(float) * v);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI for the Python test harness (oracle/oracle.py).
+// ---------------------------------------------------------------------------
+extern "C" {
+
+void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+
+void or_net_random_doubles(int seed, int n, double* out) {
+    NetRandom r(seed);
+    for (int i = 0; i < n; i++) out[i] = r.next_double();
+}
+
+void or_pcg32_ids(int seed, int max_excl, int n, int* out) {
+    Pcg32 r(seed);
+    for (int i = 0; i < n; i++) out[i] = r.next(max_excl);
+}
+
+int64_t or_param_count(int V, int ctx, int d, int L, int H) {
+    return make_layout(Cfg{V, ctx, d, L, H}).total;
+}
+
+// GptModel ctor init (GptModel.cs:38-99) from new Random(seed), registry order.
+void or_init_weights(int V, int ctx, int d, int L, int H, int seed, float* W) {
+    Cfg c{V, ctx, d, L, H};
+    Layout lay = make_layout(c);
+    NetRandom rng(seed);
+    const float std_ = 0.02f;
+    const float resid = 0.02f / std::sqrt(2.f * (float)L);
+    std::memset(W, 0, sizeof(float) * lay.total);
+    fill_normal(W + lay.tok, (int64_t)V * d, rng, std_);
+    fill_normal(W + lay.pos, (int64_t)ctx * d, rng, std_);
+    for (int i = 0; i < L; i++) {
+        const auto& B = lay.blk[i];
+        for (int e = 0; e < d; e++) W[B.ln1w + e] = 1.f;
+        fill_normal(W + B.qkvw, (int64_t)d * 3 * d, rng, std_);
+        fill_normal(W + B.projw, (int64_t)d * d, rng, resid);
+        for (int e = 0; e < d; e++) W[B.ln2w + e] = 1.f;
+        fill_normal(W + B.fcw, (int64_t)d * 4 * d, rng, std_);
+        fill_normal(W + B.mpw, (int64_t)4 * d * d, rng, resid);
+    }
+    for (int e = 0; e < d; e++) W[lay.lnfw + e] = 1.f;
+}
+
+// Elementary kernels, exposed for the known-answer tests.
+void or_matmul_nn(const float* a, const float* b, float* y, int M, int K, int N) { matmul_nn(a, b, y, M, K, N); }
+void or_matmul_nt(const float* a, const float* b, float* y, int M, int K, int N) { matmul_nt(a, b, y, M, K, N); }
+float or_dot(const float* x, const float* y, int n) { return dot_net(x, y, n); }
+void or_layernorm(const float* x, const float* w, const float* b, float* out, int rows, int cols, float eps) {
+    layernorm(x, w, b, out, rows, cols, eps);
+}
+void or_softmax(float* x, int rows, int cols) { softmax_rows(x, rows, cols); }
+void or_gelu(const float* x, float* y, int n) {
+    for (int i = 0; i < n; i++) y[i] = gelu(x[i]);
+}
+int or_greedy(const float* l, int v) { return greedy(l, v); }
+int or_sample(const float* l, int v, float temperature, int top_k, double u01) {
+    return sample(l, v, temperature, top_k, u01);
+}
+void or_apply_repetition_controls(float* l, int v, const int* hist, int n, float penalty, int ngram) {
+    apply_repetition_controls(l, v, hist, n, penalty, ngram);
+}
+
+// GptModel.Forward for one window: logits [T, V].
+void or_forward(int V, int ctx, int d, int L, int H, const float* W, const int* ids, int T, float* logits) {
+    Cfg c{V, ctx, d, L, H};
+    forward_full(c, make_layout(c), W, ids, T, logits);
+}
+
+// Sampler.Generate (Sampler.cs:78-109) for one sequence.
+//   uniforms: one NextDouble per sampled step (consumed only when temperature > 0)
+//   kv_cached: 0 = reference algorithm (full recompute), 1 = KV-cached restatement
+//   logits_out: optional [max_new, V] raw ForwardLast logits per step
+// Returns the number of tokens produced (stops after yielding eos when eos >= 0).
+int or_generate(int V, int ctx, int d, int L, int H, const float* W, const int* prompt, int n_prompt,
+                int max_new, float temperature, int top_k, const double* uniforms, int eos,
+                float penalty, int ngram, int kv_cached, int* out_ids, float* logits_out) {
+    Cfg c{V, ctx, d, L, H};
+    Layout lay = make_layout(c);
+    std::vector<int> window(prompt, prompt + n_prompt);
+    std::vector<float> logits((size_t)ctx * V), last(V), adj(V);
+    Cached cache(c, W);
+    bool need_prefill = true;
+    int produced = 0, draws = 0;
+    for (int n = 0; n < max_new; n++) {
+        if ((int)window.size() > ctx) {
+            window.erase(window.begin(), window.begin() + (window.size() - ctx));
+            need_prefill = true;  // positions restart at 0 (Sampler.cs:93-94)
+        }
+        int T = (int)window.size();
+        if (!kv_cached) {
+            forward_full(c, lay, W, window.data(), T, logits.data());
+            std::memcpy(last.data(), &logits[(size_t)(T - 1) * V], sizeof(float) * V);
+        } else if (need_prefill) {
+            cache.len = 0;
+            cache.rows(window.data(), T, last.data());
+            need_prefill = false;
+        } else {
+            cache.rows(&window[T - 1], 1, last.data());
+        }
+        if (logits_out) std::memcpy(logits_out + (size_t)n * V, last.data(), sizeof(float) * V);
+        const float* sl = last.data();
+        if (penalty != 1.f || ngram > 0) {
+            adj = last;
+            apply_repetition_controls(adj.data(), V, window.data(), T, penalty, ngram);
+            sl = adj.data();
+        }
+        double u = 0.0;
+        if (temperature > 0.f) u = uniforms[draws++];
+        int next = sample(sl, V, temperature, top_k, u);
+        out_ids[produced++] = next;
+        window.push_back(next);
+        if (eos >= 0 && next == eos) break;
+    }
+    return produced;
+}
+
+}  // extern "C"

@@ -1,0 +1,184 @@
+"""Parity of the HIP token loop with the CPU oracle, through the C ABI.
+
+Bars: greedy token ids bit-identical; per-step logits
+within rel/abs 1e-4 for fp32 (|a-e| <= tol*max(1,|e|), the reference's
+GpuBackendTests.NearRel metric, tests/LLM.Core.Tests/GpuBackendTests.cs:83-102).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+
+
+def rel_err(a, e):
+    a = np.asarray(a, np.float64)
+    e = np.asarray(e, np.float64)
+    return float(np.max(np.abs(a - e) / np.maximum(1.0, np.abs(e))))
+
+
+@pytest.fixture(scope="module")
+def backend(fhp):
+    be = fhp.HipBackend(0)
+    print(f"device: {be.device_name}, {be.compute_units} CUs", flush=True)
+    yield be
+    be.dispose()
+
+
+def make_model(fhp, oracle, backend, shape, seed, batch=1, dtype="f32"):
+    cfg = fhp.ModelConfig(*shape)
+    ocfg = oracle.Config(*shape)
+    w = oracle.init_weights(ocfg, seed)
+    m = fhp.GptModel(cfg, backend, batch=batch, dtype=dtype)
+    m.load_weights(w)
+    return m, ocfg, w
+
+
+@pytest.mark.parametrize("prompt,steps", [([1, 2], 12), (list(np.arange(12) % 32), 6), ([3, 1], 1)])
+def test_tiny_generate_with_slides(fhp, oracle, backend, prompt, steps):
+    # InferenceTests.Small; the first case slides after 6 steps, the second starts past ctx
+    m, oc, w = make_model(fhp, oracle, backend, (32, 8, 16, 2, 2), 8)
+    ids, lg = fhp.Sampler.generate(m, prompt, steps, 0.0, 0, None, return_logits=True)
+    rids, rlg = oracle.generate(oc, w, prompt, steps, return_logits=True)
+    np.testing.assert_array_equal(ids, rids)
+    assert rel_err(lg, rlg) <= TOL_F32
+    m.dispose()
+
+
+def test_forward_last_matches_golden(fhp, oracle, backend):
+    g = np.load(os.path.join(GOLDEN, "tiny_forward.npz"))
+    m, oc, w = make_model(fhp, oracle, backend, (32, 8, 16, 2, 2), 6)
+    out = m.forward_last(g["ids"])
+    assert out.shape == (1, 32)
+    assert rel_err(out[0], g["logits"][-1]) <= TOL_F32
+    m.dispose()
+
+
+def test_init_random_matches_oracle_bitwise(fhp, oracle, backend):
+    shape = (2256, 128, 128, 4, 4)
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend, seed=1234)
+    np.testing.assert_array_equal(m.read_weights(), oracle.init_weights(oracle.Config(*shape), 1234))
+    m.dispose()
+
+
+def test_c1_greedy_matches_golden(fhp, oracle, backend):
+    g = np.load(os.path.join(GOLDEN, "c1_greedy.npz"))
+    m = fhp.GptModel(fhp.ModelConfig(2256, 128, 128, 4, 4), backend, seed=1234)
+    ids, lg = fhp.Sampler.generate(m, g["prompt"], 200, 0.0, 0, None, return_logits=True)
+    np.testing.assert_array_equal(ids, g["ids"])
+    got_top = np.take_along_axis(lg, g["top5_ids"].astype(np.int64), axis=1)
+    assert rel_err(got_top, g["top5_logits"]) <= TOL_F32
+    assert rel_err(lg[g["full_steps"]], g["full_logits"]) <= TOL_F32
+    t = fhp.Sampler.last_timing
+    assert t["cached_steps"] == 112 and t["reprefill_steps"] == 87  # slide from step 113 on
+    m.dispose()
+
+
+def test_c2_greedy_matches_oracle(fhp, oracle, backend):
+    # Forge-98M shape, fp32, prompt 64 + 256 greedy
+    shape = (16384, 1024, 768, 12, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234)
+    prompt = fhp.TrainingRandom(42).ids(16384, 64)
+    ids, lg = fhp.Sampler.generate(m, prompt, 256, 0.0, 0, None, return_logits=True)
+    oracle.set_threads(8)
+    rids, rlg = oracle.generate(oc, w, prompt, 256, return_logits=True)
+    top2 = np.sort(rlg, axis=1)[:, -2:]
+    print(f"min top-2 margin {float(np.min(top2[:, 1] - top2[:, 0])):.4g}", flush=True)
+    np.testing.assert_array_equal(ids, rids)
+    err = rel_err(lg, rlg)
+    print(f"max logit rel/abs err over 256 steps: {err:.3g}", flush=True)
+    assert err <= TOL_F32
+    m.dispose()
+
+
+def test_forward_last_batch_matches_oracle(fhp, oracle, backend):
+    shape = (16384, 1024, 768, 12, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 77, batch=2)
+    r = fhp.TrainingRandom(5)
+    ids = np.stack([r.ids(16384, 40), r.ids(16384, 40)])
+    out = m.forward_last(ids)
+    for b in range(2):
+        assert rel_err(out[b], oracle.forward(oc, w, ids[b])[-1]) <= TOL_F32
+    m.dispose()
+
+
+def test_sampler_exact_on_same_logits(fhp, oracle, backend):
+    """Given the same logits, history and uniform, the device sampler returns the
+    oracle's id (Sampler.cs:29-69, 111-165), including top-k ties and bans."""
+    rng = np.random.default_rng(11)
+    cases = 0
+    for trial in range(60):
+        V = int(rng.choice([7, 100, 2256, 16384]))
+        lg = (rng.standard_normal(V) * 2).astype(np.float32)
+        if trial % 3 == 0:
+            lg = np.round(lg, 1).astype(np.float32)  # ties
+        hist = rng.integers(0, min(V, 50), size=int(rng.integers(0, 80))).astype(np.int32)
+        T = float(rng.choice([0.0, 0.7, 1.0]))
+        k = int(rng.choice([0, 1, 30, V - 1, V + 3]))
+        pen = float(rng.choice([1.0, 1.1, 2.0]))
+        ng = int(rng.choice([0, 1, 2, 4]))
+        u = float(rng.random())
+        dev = fhp.DeviceBuffer.from_array(backend, lg.astype(np.float32))
+        got = fhp.Sampler.sample_device_logits(backend, dev.ptr, V, hist, T, k, u, pen, ng)
+        dev.free()
+        adj = oracle.apply_repetition_controls(lg, hist, pen, ng) if (pen != 1.0 or ng > 0) else lg
+        want = oracle.sample(adj, T, k, u)
+        assert got == want, (trial, V, T, k, pen, ng)
+        cases += 1
+    assert cases == 60
+
+
+def test_c3_sampling_path(fhp, oracle, backend):
+    """T 0.7, top-k 30, repetition 1.1, no-repeat-ngram 4, prompt 32 + 512.
+
+    Every step: the oracle's sampler applied to the GPU's logits, the GPU's window
+    and the same uniform returns the GPU's id.  The two trajectories agree until
+    the first step whose decision the fp32 logit tolerance can flip (reported).
+    """
+    shape = (16384, 1024, 768, 12, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234)
+    prompt = fhp.TrainingRandom(42).ids(16384, 32)
+    u = fhp.Random(1).next_doubles(512)
+    ids, lg = fhp.Sampler.generate(m, prompt, 512, 0.7, 30, fhp.Random(1), repetition_penalty=1.1,
+                                   no_repeat_ngram_size=4, return_logits=True)
+    assert len(ids) == 512
+    window = list(prompt)
+    for n in range(512):
+        adj = oracle.apply_repetition_controls(lg[n], window[-1024:], 1.1, 4)
+        assert oracle.sample(adj, 0.7, 30, float(u[n])) == ids[n], f"step {n}"
+        window.append(int(ids[n]))
+    oracle.set_threads(8)
+    rids, rlg = oracle.generate(oc, w, prompt, 512, temperature=0.7, top_k=30, uniforms=u, penalty=1.1, ngram=4,
+                                return_logits=True)
+    same = int(np.argmax(ids != rids)) if np.any(ids != rids) else 512
+    print(f"C3: GPU and oracle trajectories agree for {same}/512 steps", flush=True)
+    assert rel_err(lg[:same + (1 if same < 512 else 0)], rlg[:same + (1 if same < 512 else 0)]) <= TOL_F32
+    assert same >= 64
+    m.dispose()
+
+
+def test_batched_decode_matches_single_sequences(fhp, oracle, backend):
+    shape = (2256, 128, 128, 4, 4)
+    B = 6
+    m, oc, w = make_model(fhp, oracle, backend, shape, 21, batch=B)
+    r = fhp.TrainingRandom(3)
+    prompts = np.stack([r.ids(2256, 20) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, 40, 0.0, 0, None, return_logits=True)
+    for b in range(B):
+        rids, rlg = oracle.generate(oc, w, prompts[b], 40, return_logits=True)
+        np.testing.assert_array_equal(ids[b], rids)
+        assert rel_err(lg[b], rlg) <= TOL_F32
+    m.dispose()
+
+
+def test_eos_stops_each_sequence(fhp, oracle, backend):
+    m, oc, w = make_model(fhp, oracle, backend, (32, 8, 16, 2, 2), 10)
+    first = int(fhp.Sampler.generate(m, [3, 1], 1, 0.0, 0, None)[0])
+    out = fhp.Sampler.generate(m, [3, 1], 10, 0.0, 0, None, eos_id=first)
+    assert list(out) == [first]
+    m.dispose()
