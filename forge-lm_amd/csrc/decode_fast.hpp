@@ -1,4 +1,4 @@
-// decode_fast.hpp -- fused batch-1 fp32 decode step (see decode_fast.hip).
+// decode_fast.hpp -- persistent batch-1 fp32 decode step (decode_fast.hip).
 #pragma once
 
 #include "../../include/forge_hip.h"
@@ -6,15 +6,49 @@
 
 namespace fh {
 
-// Holds the device state of the fused decode path for one session.  When the
-// session's shape is outside what the fused kernels were built for, `enabled`
-// stays false and the generic kernels run instead.
+// Device state of the persistent decode path for one session.  It runs one
+// batch-1 fp32 decode step per launch: all layers, the tied head and (in
+// greedy mode) the argmax, with dataflow hand-offs between phases.  Sessions
+// whose shape it was not built for keep `enabled` false and use the generic
+// kernels.
 struct FastDecode {
   bool enabled = false;
-  int init(hipStream_t st, const fh_model_desc& d, int compute_units);
-  int on_weights_loaded();
-  int enqueue(hipStream_t st, const RowSrc& src);
+  int D = 0, H = 0, L = 0, V = 0, C = 0, ctx = 0;
+  int blocks = 0;
+  int device = 0;
+  float* tiles = nullptr;            // per-block weight tiles, column-major
+  float* vecs = nullptr;             // LayerNorm parameters and biases at fixed offsets
+  char* uc = nullptr;                // uncached hand-off area (pairs, attention partials, argmax)
+  size_t xch_bytes = 0;
+  void* ctl = nullptr;  // launch counter (word 0), error word (16), per-head arrival counters (32..)
+  unsigned long long* trace = nullptr;  // timestamps of the last step (FORGE_HIP_TRACE=1)
+  size_t tile_floats = 0;
+
+  int init(const fh_model_desc& d, int compute_units);
+  // Builds the tiles from the registry tensors (host array of device fp32 pointers, registry order).
+  int build(hipStream_t st, const float* const* params);
+  struct Step {
+    RowSrc src;          // decode row: tok_off = pos_off = P-1, pos_mul = 1
+    const float* tok_emb;
+    const float* pos_emb;
+    float* kcache;       // [L][H][ctx][hd]
+    float* vcache;
+    float* logits;       // [V] out
+    int* out_ids;        // [max_new]
+    int* out_counts;     // [1]
+    int max_new;
+    int eos;
+    int greedy;          // 1: argmax + history update inside the kernel
+    int* tokens;         // mutable views of src.tokens / src.step
+    int* step;
+  };
+  int enqueue(hipStream_t st, const Step& s);
+  int check_error();
+  int reset();  // fresh launch counter, cleared hand-off area and error word
   void release();
+
+ private:
+  int reset_state();
 };
 
 }  // namespace fh

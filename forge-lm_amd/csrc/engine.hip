@@ -20,6 +20,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -135,6 +136,8 @@ struct fh_context {
   int* s_ints = nullptr;  // tokens | step | done | out | count
   int s_V = 0, s_hist = 0;
   double* s_u = nullptr;
+  int sessions = 0;              // live sessions on this context
+  bool destroy_pending = false;  // fh_context_destroy ran while sessions were alive
 };
 
 // ---------------------------------------------------------------------------
@@ -190,6 +193,9 @@ struct fh_session {
   uint64_t buf_gen = 1;
   // fast decode path state
   FastDecode fast;
+  bool fast_allowed = true;  // FORGE_HIP_FUSED_DECODE=0 at session creation selects the generic kernels
+  bool counted = false;      // holds a reference on its context
+  bool use_fast() const { return fast.enabled && fast_allowed; }
   // graphs
   CachedGraph g_decode, g_reprefill;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -368,8 +374,28 @@ int enqueue_decode_step(fh_session* s, const StepPlan& p) {
   hipStream_t st = s->ctx->stream;
   const int B = s->B(), D = s->d.d_model;
   RowSrc src{s->tokens, s->step, p.tok_stride, p.P - 1, p.P - 1, 1};
-  if (s->fast.enabled) {
-    FH_TRY(s->fast.enqueue(st, src));
+  if (s->use_fast()) {
+    // greedy without repetition controls or a logits dump: the argmax runs
+    // inside the decode kernel and no sampler launch follows
+    const bool greedy = !(p.opts->temperature > 0.f) && p.opts->repetition_penalty == 1.f &&
+                        p.opts->no_repeat_ngram == 0 && s->dump == nullptr;
+    FastDecode::Step fs{};
+    fs.src = src;
+    fs.tok_emb = s->v(s->idx_tok());
+    fs.pos_emb = s->v(s->idx_pos());
+    fs.kcache = reinterpret_cast<float*>(s->kc);
+    fs.vcache = reinterpret_cast<float*>(s->vc);
+    fs.logits = s->logits;
+    fs.out_ids = s->out_ids;
+    fs.out_counts = s->out_counts;
+    fs.max_new = p.max_new;
+    fs.eos = p.opts->eos_id;
+    fs.greedy = greedy ? 1 : 0;
+    fs.tokens = s->tokens;
+    fs.step = s->step;
+    int rc = s->fast.enqueue(st, fs);
+    if (rc != FH_OK) return set_err(rc, "fused decode step launch failed: %s", hipGetErrorString(hipGetLastError()));
+    if (greedy) return FH_OK;
   } else {
     LAUNCH(launch_embed<WT>(st, src, B, 1, s->w<WT>(s->idx_tok()), s->w<WT>(s->idx_pos()), D, s->d.vocab_size,
                             s->d.context_length, s->x));
@@ -460,7 +486,12 @@ int upload_weights(fh_session* s, const float* const* tensors) {
   s->loaded = true;
   drop_graph(s->g_decode);
   drop_graph(s->g_reprefill);
-  return s->fast.on_weights_loaded();
+  if (!s->fast.enabled) return FH_OK;
+  std::vector<const float*> ptrs;
+  for (size_t i = 0; i < s->reg.size(); i++) ptrs.push_back(s->v(i));
+  const int rc = s->fast.build(s->ctx->stream, ptrs.data());
+  if (rc != FH_OK) return set_err(rc, "building the fused decode tiles failed");
+  return FH_OK;
 }
 
 }  // namespace
@@ -499,8 +530,7 @@ int fh_context_create(int device, fh_context** out) {
   return FH_OK;
 }
 
-int fh_context_destroy(fh_context* c) {
-  if (!c) return FH_OK;
+static void context_free(fh_context* c) {
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
   dev_free(c->s_work);
@@ -508,6 +538,17 @@ int fh_context_destroy(fh_context* c) {
   dev_free(c->s_u);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
+}
+
+// Sessions keep their context alive: destroying a context that still has
+// sessions defers the release to the last fh_session_destroy.
+int fh_context_destroy(fh_context* c) {
+  if (!c) return FH_OK;
+  if (c->sessions > 0) {
+    c->destroy_pending = true;
+    return FH_OK;
+  }
+  context_free(c);
   return FH_OK;
 }
 
@@ -620,7 +661,12 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
     hipError_t he = hipEventCreate(&e);
     if (he != hipSuccess) return fail(set_err(FH_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(he)));
   }
-  if ((rc = sp->fast.init(sp->ctx->stream, *desc, c->props.multiProcessorCount)) != FH_OK) return fail(rc);
+  const char* fused_env = getenv("FORGE_HIP_FUSED_DECODE");
+  sp->fast_allowed = !(fused_env && fused_env[0] == '0');
+  if (sp->fast_allowed && (rc = sp->fast.init(*desc, c->props.multiProcessorCount)) != FH_OK)
+    return fail(set_err(rc, "allocating the fused decode state failed"));
+  c->sessions++;
+  sp->counted = true;
   *out = s.release();
   return FH_OK;
 }
@@ -643,7 +689,10 @@ int fh_session_destroy(fh_session* s) {
   dev_free(s->part); dev_free(s->apart); dev_free(s->logits); dev_free(s->work);
   dev_free(s->step); dev_free(s->done); dev_free(s->out_counts);
   dev_free(s->tokens); dev_free(s->out_ids); dev_free(s->uniforms); dev_free(s->dump);
+  fh_context* c = s->ctx;
+  const bool counted = s->counted;
   delete s;
+  if (counted && --c->sessions == 0 && c->destroy_pending) context_free(c);
   return FH_OK;
 }
 
@@ -818,6 +867,10 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   if (logits_dump)
     HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * max_new * V, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  if (s->use_fast() && n_dec > 0 && s->fast.check_error() != FH_OK) {
+    s->fast.reset();
+    return set_err(FH_ERR_HIP, "fused decode step: a grid barrier wait exceeded its spin limit (results discarded)");
+  }
   for (int b = 0; b < B; b++)
     if (out_counts[b] < 0) out_counts[b] = max_new;
   float ms0 = 0, ms1 = 0;
@@ -827,6 +880,16 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   s->t_decode = ms1;
   s->n_cached = n_dec;
   s->n_reprefill = n_re;
+  return FH_OK;
+}
+
+// Debug helper (not part of the public header): block-0 timestamps of the last
+// fused decode step when the session was created with FORGE_HIP_TRACE=1.
+int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n) {
+  if (!s || !out || n < 0) return set_err(FH_ERR_INVALID, "bad argument");
+  if (!s->fast.trace) return set_err(FH_ERR_STATE, "tracing is off (set FORGE_HIP_TRACE=1 before creating the session)");
+  HIP_TRY(hipStreamSynchronize(s->ctx->stream));
+  HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256), hipMemcpyDeviceToHost));
   return FH_OK;
 }
 

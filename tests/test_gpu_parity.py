@@ -96,6 +96,31 @@ def test_c2_greedy_matches_oracle(fhp, oracle, backend):
     m.dispose()
 
 
+def test_c2_generic_decode_path_matches_oracle(fhp, oracle, backend, monkeypatch):
+    """The same workload on the generic multi-kernel decode path (fused step off)."""
+    monkeypatch.setenv("FORGE_HIP_FUSED_DECODE", "0")
+    shape = (16384, 1024, 768, 12, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 99)
+    prompt = fhp.TrainingRandom(7).ids(16384, 48)
+    ids, lg = fhp.Sampler.generate(m, prompt, 24, 0.0, 0, None, return_logits=True)
+    rids, rlg = oracle.generate(oc, w, prompt, 24, return_logits=True)
+    np.testing.assert_array_equal(ids, rids)
+    assert rel_err(lg, rlg) <= TOL_F32
+    m.dispose()
+
+
+def test_fused_greedy_without_dump_matches_dump_run(fhp, oracle, backend):
+    """Greedy without a logits dump takes the in-kernel argmax; ids equal the dumped run's."""
+    shape = (16384, 1024, 768, 12, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 5)
+    prompt = fhp.TrainingRandom(11).ids(16384, 20)
+    ids_fast = fhp.Sampler.generate(m, prompt, 64, 0.0, 0, None)
+    ids_dump, _ = fhp.Sampler.generate(m, prompt, 64, 0.0, 0, None, return_logits=True)
+    np.testing.assert_array_equal(ids_fast, ids_dump)
+    np.testing.assert_array_equal(ids_fast, oracle.generate(oc, w, prompt, 64))
+    m.dispose()
+
+
 def test_forward_last_batch_matches_oracle(fhp, oracle, backend):
     shape = (16384, 1024, 768, 12, 12)
     m, oc, w = make_model(fhp, oracle, backend, shape, 77, batch=2)
