@@ -41,7 +41,7 @@ def decode_bytes_per_step(c, attended: float, batch: int = 1, esize: int = 4) ->
     return weights + batch * per_seq
 
 
-def cpu_baseline(weights_seed: int, prompt, gpu_ids, budget_tokens: int = 16):
+def cpu_baseline(weights_seed: int, prompt, gpu_ids, budget_tokens: int = 96):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     threads = min(16, os.cpu_count() or 1)
@@ -60,18 +60,56 @@ def cpu_baseline(weights_seed: int, prompt, gpu_ids, budget_tokens: int = 16):
     }
 
 
+def copy_calibration(mib: int, reps: int) -> dict:
+    """Times the library's plain copy kernel (fh_buffer_copy) on `mib` MiB: the
+    known-size kernel whose FETCH_SIZE / WRITE_SIZE counters scale the decode
+    kernel's counters to bytes."""
+    import forge_hip as fhp
+    nbytes = mib << 20
+    be = fhp.HipBackend(0)
+    src, dst = fhp.DeviceBuffer(be, nbytes), fhp.DeviceBuffer(be, nbytes)
+    dst.copy_from(src)  # warm-up
+    ms = [dst.copy_from(src) for _ in range(reps)]
+    src.free()
+    dst.free()
+    be.dispose()
+    best = min(ms)
+    return {"copy_bytes": nbytes, "reps": reps, "ms_min": round(best, 4), "ms_mean": round(sum(ms) / len(ms), 4),
+            "read_plus_write_GBs": round(2 * nbytes / best / 1e6, 1)}
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "decode_step_c2_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:") and kernel in line:
+                    return int(line.split(":", 1)[1].split()[0])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=96,
+                    help="tokens of the workload the CPU baseline runs (about 15-25 s on 16 cores)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only time the plain copy kernel on MIB MiB and print its line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs one GPU only: the token loop of one batch-1 sequence is a single-GPU "
               f"workload and this build has no multi-GPU path (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        print(json.dumps(copy_calibration(args.copy_calibration, max(1, args.steps))), flush=True)
+        return
 
     import numpy as np
     import forge_hip as fhp
@@ -100,6 +138,8 @@ def main():
     step_bytes = decode_bytes_per_step(C2, attended)
     achieved = step_bytes / avg_step_s / 1e9
     value = args.steps * NEW_TOKENS / wall
+    fused = os.environ.get("FORGE_HIP_FUSED_DECODE", "1") != "0"
+    kernel = "k_decode_step<768>" if fused else "decode step graph (generic kernels)"
     out = {
         "metric": "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)",
         "value": round(value, 2),
@@ -120,9 +160,10 @@ def main():
         "decode_us_per_token": round(avg_step_s * 1e6, 2),
         "prefill_tok_s": round(PROMPT_LEN / (float(np.mean(prefill_ms)) / 1e3), 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "one decode step (all kernels of the step graph)",
-                     "bytes_per_launch": int(step_bytes)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": profiled_traffic(kernel) if fused else None,
+                     "kernel": kernel, "bytes_per_launch": int(step_bytes),
+                     "launch_us": round(avg_step_s * 1e6, 2)},
         "device": be.device_name,
     }
     if not args.no_cpu:

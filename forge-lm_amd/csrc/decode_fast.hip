@@ -3,10 +3,12 @@
 // One launch runs a whole decode step of the token loop (GptModel.ForwardLast
 // on the cached window, src/LLM.Core/Model/GptModel.cs:202-222, then
 // Sampler.Greedy, src/LLM.Core/Inference/Sampler.cs:14-20): 256 blocks (one
-// per CU, round-robin over the 8 XCDs) x 512 threads.  Per layer five phases:
+// per CU, round-robin over the 8 XCDs) x 256 threads (waves 0..2 hold weight
+// tiles, wave 3 is the control wave).  Per layer five phases:
 //   A  LN1 + QKV columns (9 of 2304 per block); new K/V row into the cache
-//   B  decode attention: (head, key chunk) blocks, online softmax
-//   C  combine attention chunks + attn.proj columns + residual -> x2
+//   B  decode attention: (head, key chunk) blocks, online softmax; the last of
+//      a head's chunk blocks to arrive combines the chunks into the head's o
+//   C  attn.proj columns + residual -> x2
 //   D  LN2 + mlp.fc columns + GELU -> h
 //   E  mlp.proj columns + residual -> x
 // then LN_f + the tied head (64 vocab rows per block) and, in greedy mode, the
@@ -16,19 +18,20 @@
 // Dataflow instead of grid barriers: every value handed from one phase to the
 // next is stored as a 64-bit (value, tag) pair in uncached device memory, the
 // tag being this launch's sequence number for the producing phase.  A
-// consumer's control wave (wave 7) re-reads the pairs it needs until every tag
-// matches, then copies the values to LDS; one memory round trip after the last
+// consumer's control wave re-reads the pairs it needs until every tag matches,
+// then copies the values to LDS; one memory round trip after the last
 // producer's store, instead of a barrier plus a separate read.  Because every
 // phase reads the outputs of all blocks of the phase before it, no block can
 // run a full phase ahead of another, so no buffer is overwritten while a
-// reader still needs it.  Attention partials are written data-first, tag-last.
+// reader still needs it.  Attention partials and argmax records are written
+// data first, tag (or arrival count) last.
 //
-// Waves 0..6 hold weight tiles in registers: each block's tiles were re-laid
-// out once into contiguous column-major blocks, and the next phase's tile is
-// requested as soon as the current one is consumed, so HBM streams while the
-// control wave waits for the hand-off.  Attention K/V rows of the cached
-// positions are prefetched into registers during phase A.  Every wait is
-// bounded: past the spin limit the error word is set and all blocks leave.
+// The data waves hold weight tiles in registers: each block's tiles were
+// re-laid out once into contiguous column-major blocks, and the next phase's
+// tile is requested as soon as the current one is consumed, so HBM streams
+// while the control wave waits for the hand-off.  Cached K/V rows are requested
+// before q arrives.  Every wait is bounded: past the spin limit the error word
+// is set and all blocks leave.
 #include <math.h>
 #include <stdlib.h>
 

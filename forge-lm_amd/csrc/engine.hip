@@ -554,7 +554,12 @@ int fh_context_destroy(fh_context* c) {
 
 int fh_context_info(fh_context* c, char* name, size_t name_len, uint64_t* total_mem, int32_t* cus) {
   if (!c) return set_err(FH_ERR_INVALID, "context is null");
-  if (name && name_len) snprintf(name, name_len, "%s (%s)", c->props.name, c->props.gcnArchName);
+  if (name && name_len) {
+    if (c->props.name[0])
+      snprintf(name, name_len, "%s (%s)", c->props.name, c->props.gcnArchName);
+    else
+      snprintf(name, name_len, "%s", c->props.gcnArchName);
+  }
   if (total_mem) *total_mem = c->props.totalGlobalMem;
   if (cus) *cus = c->props.multiProcessorCount;
   return FH_OK;
@@ -592,6 +597,27 @@ int fh_buffer_read(fh_context* c, void* dst, const void* src_dev, size_t bytes) 
   HIP_TRY(hipSetDevice(c->device));
   HIP_TRY(hipMemcpyAsync(dst, src_dev, bytes, hipMemcpyDeviceToHost, c->stream));
   HIP_TRY(hipStreamSynchronize(c->stream));
+  return FH_OK;
+}
+
+int fh_buffer_copy(fh_context* c, void* dst_dev, const void* src_dev, size_t bytes, float* ms_out) {
+  if (!c || !dst_dev || !src_dev) return set_err(FH_ERR_INVALID, "null argument");
+  if (((uintptr_t)dst_dev | (uintptr_t)src_dev) % 16)
+    return set_err(FH_ERR_INVALID, "device buffers must be 16-byte aligned");
+  HIP_TRY(hipSetDevice(c->device));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (ms_out) {
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(hipEventRecord(e0, c->stream));
+  }
+  hipError_t e = launch_copy(c->stream, dst_dev, src_dev, bytes);
+  if (e == hipSuccess && ms_out) e = hipEventRecord(e1, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess && ms_out) e = hipEventElapsedTime(ms_out, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  HIP_TRY(e);
   return FH_OK;
 }
 

@@ -697,6 +697,16 @@ __global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
 
 #pragma clang fp contract(on)
 
+// Plain device copy: 16-byte vector loads and stores over a grid-stride loop,
+// then the byte tail.  Also the calibration kernel for HBM traffic counters.
+__global__ void k_copy_bytes(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16,
+                             const unsigned char* __restrict__ src_tail, unsigned char* __restrict__ dst_tail,
+                             int tail) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+  if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
+}
+
 // ---------------------------------------------------------------------------
 // launch wrappers
 // ---------------------------------------------------------------------------
@@ -793,6 +803,19 @@ hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* 
   FH_CHECK_ARG(B > 0 && d > 0 && d <= 1024 && d % VEC == 0 && V > 0 && xn && E && logits);
   const int blocks = min(1024, (V + 3) / 4);
   hipLaunchKernelGGL(k_head<WT>, dim3(blocks), dim3(256), 0, st, xn, B, d, E, V, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes) {
+  FH_CHECK_ARG(dst && src && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0);
+  if (bytes == 0) return hipSuccess;
+  const size_t n16 = bytes / 16;
+  const int tail = (int)(bytes % 16);
+  const size_t want = (n16 + 255) / 256;
+  const unsigned blocks = (unsigned)(want < 8192 ? (want ? want : 1) : 8192);
+  hipLaunchKernelGGL(k_copy_bytes, dim3(blocks), dim3(256), 0, st, static_cast<const uint4*>(src),
+                     static_cast<uint4*>(dst), n16, static_cast<const unsigned char*>(src) + n16 * 16,
+                     static_cast<unsigned char*>(dst) + n16 * 16, tail);
   return hipGetLastError();
 }
 

@@ -53,6 +53,9 @@ hipError_t launch_attn_decode(hipStream_t st, RowSrc src, const float* qkv, int 
 template <typename WT>
 hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* E, int V, float* logits);
 
+// dst[0..bytes) = src[0..bytes) on the device (both 16-byte aligned).
+hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);
+
 struct SampleArgs {
   const float* logits;  // [B][V] raw ForwardLast logits
   float* work;          // [B][V] scratch

@@ -102,6 +102,11 @@ int fh_buffer_alloc(fh_context* ctx, size_t bytes, void** out_dev);
 int fh_buffer_free(fh_context* ctx, void* dev);
 int fh_buffer_write(fh_context* ctx, void* dst_dev, const void* src, size_t bytes);
 int fh_buffer_read(fh_context* ctx, void* dst, const void* src_dev, size_t bytes);
+/* ITensorBackend.Copy(src, dst) on device buffers (ITensorBackend.cs:86): one copy
+ * kernel on the context stream, synchronous.  Both pointers 16-byte aligned.  When
+ * ms_out is not NULL it receives the kernel's duration from HIP events (the
+ * bandwidth calibration of the benchmark's traffic counters). */
+int fh_buffer_copy(fh_context* ctx, void* dst_dev, const void* src_dev, size_t bytes, float* ms_out);
 
 /* session = weights + KV cache + token history + scratch for max_batch sequences */
 int fh_session_create(fh_context* ctx, const fh_model_desc* desc, fh_session** out);

@@ -10,12 +10,15 @@
 // "multiply then add" in the reference stays two roundings.
 //
 // Pinning status of each part (what checks it in tests/):
-//   NetRandom ............ parity unpinned vs .NET (no runtime here); restated
-//                          from the published subtractive generator (Knuth
-//                          TAOCP 3.2.2 / Numerical Recipes ran3).  Weights and
-//                          uniforms are generated once and fed to both this
-//                          oracle and the GPU, so GPU parity does not depend
-//                          on it.  Statistical checks only (mean/var, range).
+//   NetRandom ............ restated from the published subtractive generator
+//                          (Knuth TAOCP 3.2.2 / Numerical Recipes ran3); pinned
+//                          by published outputs of the seeded .NET generator
+//                          (new Random(1).Next() x3, new Random(0).NextDouble())
+//                          and stream statistics.  Beyond those values the
+//                          stream is parity unpinned vs .NET (no runtime here);
+//                          weights and uniforms are generated once and fed to
+//                          both this oracle and the GPU, so GPU parity does
+//                          not depend on it.
 //   Pcg32 ................ pinned by the PCG32 reference formula (O'Neill 2014)
 //                          checked in Python against an independent big-int
 //                          restatement plus the unbiased-bound rejection rule.

@@ -271,6 +271,15 @@ def test_net_random_stream_statistics(oracle):
     assert np.any(oracle.net_random_doubles(2, 100) != u[:100])
 
 
+def test_net_random_published_values(oracle):
+    # published outputs of .NET's seeded System.Random: new Random(1).Next() x3
+    # (Next() is the raw sample, NextDouble() = sample / int.MaxValue) and
+    # new Random(0).NextDouble(); a wrong seed constant, tap or sign fails these
+    r1 = oracle.net_random_doubles(1, 3)
+    assert [int(round(x * 2147483647)) for x in r1] == [534011718, 237820880, 1002897798]
+    assert abs(oracle.net_random_doubles(0, 1)[0] - 0.7262432699679598) < 1e-15
+
+
 # ---- golden vectors --------------------------------------------------------------------------
 
 def test_golden_c1_greedy(oracle):
