@@ -2,36 +2,43 @@
 //
 // One launch runs a whole decode step of the token loop (GptModel.ForwardLast
 // on the cached window, src/LLM.Core/Model/GptModel.cs:202-222, then
-// Sampler.Greedy, src/LLM.Core/Inference/Sampler.cs:14-20): 256 blocks (one
-// per CU, round-robin over the 8 XCDs) x 256 threads (waves 0..2 hold weight
-// tiles, wave 3 is the control wave).  Per layer five phases:
-//   A  LN1 + QKV columns (9 of 2304 per block); new K/V row into the cache
-//   B  decode attention: (head, key chunk) blocks, online softmax; the last of
-//      a head's chunk blocks to arrive combines the chunks into the head's o
+// Sampler.Greedy, src/LLM.Core/Inference/Sampler.cs:14-20): 256 blocks, one per
+// CU; the dispatcher deals blocks round-robin over the 8 XCDs, so block b is
+// slot b / 8 of the 32 blocks on its XCD (read from the hardware).  Each
+// block has 256 threads: waves 0..2 hold weight tiles in registers, wave 3 is
+// the control wave that collects hand-offs.  Per layer:
+//   A  LN1 + QKV: the 192 q/k/v columns of head h are computed by blocks of
+//      XCD h % 8 only, so q/k/v reach that head's attention blocks through the
+//      XCD's own L2; the new K/V row goes into the cache
+//   B  attention of head h by blocks of XCD h % 8: 64 keys per data wave
+//      (lane = key for the scores, lane = dim for P.V), 192 keys per block;
+//      a head spanning several blocks is combined by its first block
 //   C  attn.proj columns + residual -> x2
 //   D  LN2 + mlp.fc columns + GELU -> h
 //   E  mlp.proj columns + residual -> x
 // then LN_f + the tied head (64 vocab rows per block) and, in greedy mode, the
 // argmax.  At batch 1 every weight is used once per token, so the step is
-// bound by HBM bytes plus the chain of cross-CU hand-offs.
+// bound by HBM bytes plus the chain of hand-offs between phases.
 //
-// Dataflow instead of grid barriers: every value handed from one phase to the
-// next is stored as a 64-bit (value, tag) pair in uncached device memory, the
-// tag being this launch's sequence number for the producing phase.  A
-// consumer's control wave re-reads the pairs it needs until every tag matches,
-// then copies the values to LDS; one memory round trip after the last
-// producer's store, instead of a barrier plus a separate read.  Because every
-// phase reads the outputs of all blocks of the phase before it, no block can
-// run a full phase ahead of another, so no buffer is overwritten while a
-// reader still needs it.  Attention partials and argmax records are written
-// data first, tag (or arrival count) last.
+// Hand-offs without grid barriers: every value passed from one phase to the
+// next is stored as a 64-bit (value, tag) pair, the tag being this launch's
+// sequence number for the producing phase (launch counter * 128 + phase).  A
+// consumer's control wave re-reads the pairs it needs until every tag
+// matches, then copies the values to LDS.  Values that cross
+// XCDs (x, x2, h, o, the per-block argmax) live in uncached memory; values that
+// stay inside one XCD (q/k/v, attention partials) live in ordinary device
+// memory, where the XCD's L2 is the coherence point.  Reads of both bypass
+// the CU's L1 (buffer loads with the SC0|SC1 policy).  Because every consumer
+// needs the outputs of a whole phase before it, no producer can run a full
+// phase ahead of a reader, so no pair is overwritten while still needed.  The
+// launch counter only grows (also across resets), so stale pairs never match.
 //
-// The data waves hold weight tiles in registers: each block's tiles were
-// re-laid out once into contiguous column-major blocks, and the next phase's
-// tile is requested as soon as the current one is consumed, so HBM streams
-// while the control wave waits for the hand-off.  Cached K/V rows are requested
-// before q arrives.  Every wait is bounded: past the spin limit the error word
-// is set and all blocks leave.
+// The data waves hold every tile of the current layer in registers (each
+// block's columns re-laid out once into contiguous column-major tiles) and
+// request the next layer's tile as soon as the current one is consumed, so
+// HBM streams continuously while the control wave waits.  Cached K/V rows are
+// requested before x arrives.  Every wait is bounded: past the spin limit the
+// error word is set and all blocks leave.
 #include <math.h>
 #include <stdlib.h>
 
@@ -45,34 +52,56 @@ namespace fh {
 
 namespace {
 
-constexpr int NB = 256;   // blocks
-constexpr int NT = 256;   // threads per block: one wave per SIMD, so 512 registers per wave
+constexpr int NB = 256;      // blocks
+constexpr int NT = 256;      // threads per block: one wave per SIMD
 constexpr int NW = NT / 64;
 constexpr int NDW = NW - 1;  // data waves (the last wave is the control wave)
-constexpr int AC = 16;    // attention key chunks per head
-constexpr int KG = 8;     // keys per data wave per group (online softmax across groups)
-constexpr int TAGS = 128;  // tag values reserved per launch
-constexpr long SPIN_LIMIT = 300000;
+constexpr int NX = 8;        // XCDs
+constexpr int SLOTS = NB / NX;
+constexpr int KPW = 32;            // attention keys per data wave (two lanes per key)
+constexpr int KPB = KPW * NDW;     // attention keys per block
+constexpr int TAGS = 128;          // tag values reserved per launch
+constexpr int PH = 6;              // tagged phases per layer
+constexpr long SPIN_LIMIT = 400000;
+constexpr int PART = 68;           // pairs per attention partial: o[64], m, l, pad[2]
 
 __device__ __forceinline__ bool err_set(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
-__device__ __forceinline__ void raise_err(int* err) {
-  __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The first failing wait records where it was: 1 << 31 | wait << 24 | layer << 16 | block
+// (waits: 1 x, 2 q/k/v, 3 partials, 4 o, 5 x2, 6 h, 7 final x, 8 argmax).
+// A wait that gives up because another block already failed records nothing.
+enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_X2, W_H, W_XF, W_AMAX };
+__device__ __forceinline__ int err_code(int wait, int l) {
+  return (int)(0x80000000u | ((unsigned)wait << 24) | ((unsigned)(l & 0xff) << 16) | blockIdx.x);
 }
-// wait until this thread's stores are acknowledged by memory
-__device__ __forceinline__ void stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ void raise_err(int* err, int code) {
+  int expected = 0;
+  __hip_atomic_compare_exchange_strong(err, &expected, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+}
 // keeps the compiler from reusing values loaded before this point
 __device__ __forceinline__ void reload_fence() { asm volatile("" ::: "memory"); }
+// this wave's LDS writes are complete and visible to its own later reads
+__device__ __forceinline__ void wave_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
+}
 
 __device__ __forceinline__ void put_pair(uint2* dst, float v, unsigned tag) {
   *dst = make_uint2(__float_as_uint(v), tag);
 }
 
-// Reads of the hand-off area go through a raw buffer resource with the
-// system-coherent cache policy (SC0|SC1): they miss in the CU's L1 and in L2,
-// so a re-read sees other CUs' stores (uncached memory is still cached in L1
-// by plain loads).  Out-of-range offsets read as 0.
+__device__ __forceinline__ unsigned xcc_id() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
+// Reads of the hand-off areas go through a raw buffer resource with the
+// SC0|SC1 cache policy: they miss in the CU's L1, so a re-read sees other CUs'
+// stores (plain loads would keep hitting a stale L1 line).  Out-of-range
+// offsets read as 0.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 struct NcBuf {
   __amdgpu_buffer_rsrc_t r;
@@ -82,49 +111,53 @@ struct NcBuf {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 17);
     return make_uint4(v.x, v.y, v.z, v.w);
   }
-  __device__ __forceinline__ unsigned load1(int byte_off) const {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 17);
-  }
 };
 
-template <int D>
+template <int D, int H>
 struct Shape {
-  static constexpr int KC = D / 256;        // 256-float chunks per K=D column
-  static constexpr int KC4 = 4 * D / 256;   // chunks per K=4D column
-  static constexpr int QCOL = 3 * D / NB;   // qkv columns per block
-  static constexpr int PCOL = D / NB;       // attn.proj / mlp.proj columns per block
-  static constexpr int FCOL = 4 * D / NB;   // mlp.fc columns per block
-  static constexpr int QCH = QCOL * KC;
-  static constexpr int PCH = PCOL * KC;
-  static constexpr int FCH = FCOL * KC;
-  static constexpr int MCH = PCOL * KC4;
-  static constexpr int QMAX = (QCH + NDW - 1) / NDW;
-  static constexpr int PMAX = (PCH + NDW - 1) / NDW;
-  static constexpr int FMAX = (FCH + NDW - 1) / NDW;
-  static constexpr int MMAX = (MCH + NDW - 1) / NDW;
-  static constexpr int RMAX = 64;  // vocab rows per block (V <= 16384)
-  static constexpr int HMAX = (RMAX * KC + NDW - 1) / NDW;
-  static constexpr int PER = (D + NT - 1) / NT;  // LayerNorm elements per thread
-  // tile floats per block, in phase order
-  static constexpr size_t QT = (size_t)QCOL * D, PT = (size_t)PCOL * D, FT = (size_t)FCOL * D,
+  static constexpr int HD = 64;
+  static constexpr int KC = D / 256;       // 256-float chunks per K=D column
+  static constexpr int KC4 = 4 * D / 256;  // chunks per K=4D column
+  static constexpr int HPX = (H + NX - 1) / NX;  // heads per XCD (at most)
+  static constexpr int SPH = SLOTS / HPX;        // slots per head
+  static constexpr int QCMAX = 3 * HD * HPX / SLOTS;  // qkv columns per block (at most)
+  static constexpr int QCW = QCMAX / NDW;              // qkv columns per data wave (at most)
+  static constexpr int PCOL = D / NB;      // attn.proj / mlp.proj columns per block (one per data wave)
+  static constexpr int FCOL = 4 * D / NB;  // mlp.fc columns per block
+  static constexpr int FCW = FCOL / NDW;   // per data wave
+  static constexpr int RMAX = 64;          // vocab rows per block (V <= 16384)
+  // tile floats per block
+  static constexpr size_t QT = (size_t)QCMAX * D, PT = (size_t)PCOL * D, FT = (size_t)FCOL * D,
                           MT = (size_t)PCOL * 4 * D;
   static constexpr size_t LAYER = (size_t)NB * (QT + PT + FT + MT);
-  // compact vector buffer: per layer ln1.w ln1.b qkv.b proj.b ln2.w ln2.b fc.b mproj.b
-  static constexpr int V_LN1W = 0, V_LN1B = D, V_QKVB = 2 * D, V_PROJB = 5 * D, V_LN2W = 6 * D, V_LN2B = 7 * D,
-                       V_FCB = 8 * D, V_MPB = 12 * D, VL = 13 * D;
+  // compact vector buffer per layer: ln1.w ln1.b ln2.w ln2.b
+  static constexpr int V_LN1W = 0, V_LN1B = D, V_LN2W = 2 * D, V_LN2B = 3 * D, VL = 4 * D;
+  // per-block bias table per layer: qkv[QCMAX] proj[PCOL] fc[FCOL] mproj[PCOL]
+  static constexpr int B_Q = 0, B_P = QCMAX, B_F = QCMAX + PCOL, B_M = QCMAX + PCOL + FCOL, BT = 32;
+  static_assert(D == H * HD, "head_dim 64");
+  static_assert(D % 256 == 0 && D % NB == 0 && PCOL == NDW, "one proj column per data wave");
+  static_assert(QCMAX % NDW == 0 && FCOL % NDW == 0, "columns split evenly over the data waves");
+  static_assert(B_M + PCOL <= BT, "bias table row");
+  static_assert(SPH * HPX == SLOTS, "slots split evenly over an XCD's heads");
 };
 
-// exchange layout (uncached): pairs (uint2) and the attention partials
+// uncached (cross-XCD) pair layout
 template <int D>
-struct Xch {
-  static constexpr int X = 0, X2 = D, HH = 2 * D, QKV = 6 * D, O = 9 * D, NPAIR = 10 * D;  // pair offsets
-  static constexpr int AP_STRIDE = 68;  // floats per attention partial: o[64], m, l, pad[2]
+struct Xu {
+  static constexpr int X = 0, X2 = D, HH = 2 * D, O = 6 * D, NPAIR = 7 * D;
+};
+// per-XCD local pair layout: qkv of the XCD's heads, then the attention partials
+template <int D, int H>
+struct Xl {
+  using S = Shape<D, H>;
+  static constexpr int QKV = 0, PARTS = 3 * S::HD * S::HPX, STRIDE = PARTS + S::HPX * S::SPH * PART;
 };
 
 struct KParams {
   RowSrc src;
   const float* tiles;
   const float* vecs;
+  const float* btab;
   const float* tok;
   const float* pos;
   float* kc;
@@ -132,17 +165,16 @@ struct KParams {
   float* logits;
   int* out_ids;
   int* out_counts;
-  uint2* pairs;      // uncached: x, x2, h, qkv pairs
-  float* apart;      // uncached: attention partials [H*AC][68]
-  unsigned* hcnt;    // per-head arrival counters of the attention chunk blocks (agent atomics)
-  uint4* amax;       // uncached: per-block (value, index, tag, -)
-  int uc_bytes;      // size of the uncached area starting at `pairs`
-  int off_apart, off_amax;  // byte offsets of the areas above from `pairs`
-  unsigned* launch;  // launch counter (agent atomics)
+  uint2* uc;          // uncached pairs (Xu), then the argmax records
+  int uc_bytes;
+  int off_amax;       // byte offset of the argmax records in uc
+  uint2* xl;          // per-XCD pairs (Xl), ordinary device memory
+  int xl_bytes;
+  unsigned* launch;   // launch counter
   int* err;
-  int V, ctx, H, L, max_new, eos, greedy;
-  int* tokens_out;  // same buffer as src.tokens, written by the greedy argmax
-  int* step_out;    // same word as src.step
+  int V, ctx, L, max_new, eos, greedy;
+  int* tokens_out;    // same buffer as src.tokens, written by the greedy argmax
+  int* step_out;      // same word as src.step
   unsigned long long* trace;  // optional: block 0 timestamps
 };
 
@@ -150,13 +182,14 @@ __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
   if (t && blockIdx.x == 0 && threadIdx.x == (NT - 64) && i < 256) t[i] = wall_clock64();
 }
 
-// Control wave: waits until pairs[0..n) all carry `tag`, then stores the values
-// to out[0..n) (LDS).  n must be a multiple of 128 (two pairs per 16-byte load).
-// Returns false on spin-limit or a raised error.
+// Control wave: waits until pairs[pair0, pair0 + N) all carry `tag`, then
+// stores the values to out[0, N) (LDS).  One read in flight: a second poll
+// issued ahead would still be in flight when the wait ends, and reusing its
+// registers would wait for it.
 template <int N>
-__device__ bool wait_pairs(const NcBuf& nc, int pair0, unsigned tag, float* out, int* err) {
-  static_assert(N % 128 == 0, "pairs come in 16-byte loads");
-  constexpr int R = N / 128;  // 16-byte loads per lane
+__device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int* err, int code) {
+  static_assert(N % 2 == 0, "pairs come in 16-byte loads");
+  constexpr int R = (N + 127) / 128;
   const int lane = threadIdx.x & 63;
   uint4 v[R];
   long it = 0;
@@ -166,507 +199,576 @@ __device__ bool wait_pairs(const NcBuf& nc, int pair0, unsigned tag, float* out,
     for (int r = 0; r < R; r++) v[r] = nc.load4(pair0 * 8 + (r * 64 + lane) * 16);
     bool ok = true;
 #pragma unroll
-    for (int r = 0; r < R; r++) ok &= (v[r].y == tag) & (v[r].w == tag);
+    for (int r = 0; r < R; r++)
+      if (N % 128 == 0 || (r * 64 + lane) * 2 < N) ok &= (v[r].y == tag) & (v[r].w == tag);
     if (__all(ok)) break;
-    if (++it > SPIN_LIMIT || err_set(err)) {
-      if (lane == 0) raise_err(err);
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
       return false;
     }
   }
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int i = 2 * (r * 64 + lane);
-    out[i] = __uint_as_float(v[r].x);
-    out[i + 1] = __uint_as_float(v[r].z);
+    if (N % 128 == 0 || i < N)
+      *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
   }
   return true;
 }
 
-__device__ __forceinline__ float block_sum512(float v, float* red) {
-  v = wave_sum_dpp(v);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane == 0) red[w] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < NW; i++) s += red[i];
-  __syncthreads();
-  return s;
+__device__ __forceinline__ float dot4(const float4 a, const float4 b) {
+  return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
 
-// LayerNorm of xin[D] (LDS) into xout[D] (LDS) with this thread's parameters
-// w[j], b[j] for elements tid + j*NT (biased variance, eps 1e-5).
-template <int D>
-__device__ void layernorm_regs(const float* xin, float* xout, const float (&w)[Shape<D>::PER],
-                               const float (&b)[Shape<D>::PER], float* red) {
-  constexpr int PER = Shape<D>::PER;
+// LayerNorm of xin[D] (LDS) for this lane's elements k = c*256 + lane*4 + 0..3
+// (c < KC), computed by each wave on its own (biased variance, eps 1e-5,
+// ((x - mu) * rs) * w + b as CpuBackend.LayerNormForward).
+template <int KC, int D>
+__device__ __forceinline__ void ln_lane(const float* xin, const float4 (&w)[KC], const float4 (&b)[KC],
+                                        float4 (&xn)[KC]) {
+  const int lane = threadIdx.x & 63;
+  float4 xv[KC];
   float s = 0.f;
 #pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int i = threadIdx.x + j * NT;
-    if (i < D) s += xin[i];
+  for (int c = 0; c < KC; c++) {
+    xv[c] = *reinterpret_cast<const float4*>(xin + c * 256 + lane * 4);
+    s += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
   }
-  const float mu = block_sum512(s, red) / (float)D;
+  const float mu = wave_sum_dpp(s) / (float)D;
   float v = 0.f;
 #pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int i = threadIdx.x + j * NT;
-    if (i < D) {
-      const float d = xin[i] - mu;
-      v += d * d;
-    }
+  for (int c = 0; c < KC; c++) {
+    const float a = xv[c].x - mu, bb = xv[c].y - mu, cc = xv[c].z - mu, dd = xv[c].w - mu;
+    v += (a * a + bb * bb) + (cc * cc + dd * dd);
   }
-  const float var = block_sum512(v, red);
+  const float var = wave_sum_dpp(v);
   const float rs = 1.f / sqrtf(var / (float)D + 1e-5f);
 #pragma unroll
-  for (int j = 0; j < PER; j++) {
-    const int i = threadIdx.x + j * NT;
-    if (i < D) xout[i] = (xin[i] - mu) * rs * w[j] + b[j];
+  for (int c = 0; c < KC; c++) {
+    xn[c].x = (xv[c].x - mu) * rs * w[c].x + b[c].x;
+    xn[c].y = (xv[c].y - mu) * rs * w[c].y + b[c].y;
+    xn[c].z = (xv[c].z - mu) * rs * w[c].z + b[c].z;
+    xn[c].w = (xv[c].w - mu) * rs * w[c].w + b[c].w;
   }
-  __syncthreads();
 }
 
-template <int D>
-__device__ __forceinline__ void load_ln(const float* wv, const float* bv, float (&w)[Shape<D>::PER],
-                                        float (&b)[Shape<D>::PER]) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+__device__ __forceinline__ float4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
+// r[i] = chunk i of a tile (chunk = 64 lanes x float4 = 1 KB).  Loads through a
+// buffer resource: one base in scalar registers and constant offsets; with
+// real == false the resource is empty and the loads return zeros without
+// touching memory (every register is still written on every path).
+template <int N>
+__device__ __forceinline__ void load_chunks(float4 (&r)[N], const float* tile, bool real) {
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(tile, real ? N * 1024 : 0);
+  const int off = (threadIdx.x & 63) * 16;
 #pragma unroll
-  for (int j = 0; j < Shape<D>::PER; j++) {
-    const int i = min((int)threadIdx.x + j * NT, D - 1);
-    w[j] = wv[i];
-    b[j] = bv[i];
-  }
+  for (int i = 0; i < N; i++) r[i] = ld4(rs, off + i * 1024);
 }
 
-// Loads this wave's chunks of a tile (chunk = 64 lanes x float4) into registers.
-template <int MAX, int NCH>
-__device__ __forceinline__ void tile_load(float4 (&r)[MAX], const float* tile) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (w >= NDW) return;
-  const float4* t4 = reinterpret_cast<const float4*>(tile);
-#pragma unroll
-  for (int i = 0; i < MAX; i++) {
-    const int ch = min(w + NDW * i, NCH - 1);
-    r[i] = t4[ch * 64 + lane];
-  }
-}
-
-// Chunk dot products against xs (LDS): part[ch] = sum over the chunk's 256 k.
-template <int MAX, int NCH, int KCH>
-__device__ __forceinline__ void tile_dot(const float4 (&r)[MAX], const float* xs, float* part) {
-  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  if (w >= NDW) return;
-#pragma unroll
-  for (int i = 0; i < MAX; i++) {
-    const int ch = w + NDW * i;
-    if (ch < NCH) {
-      const int kc = ch % KCH;
-      const float4 xv = *reinterpret_cast<const float4*>(xs + kc * 256 + lane * 4);
-      const float p = wave_sum_dpp(r[i].x * xv.x + r[i].y * xv.y + r[i].z * xv.z + r[i].w * xv.w);
-      if (lane == 0) part[ch] = p;
-    }
-  }
-}
-
-template <int D>
+template <int D, int H>
 __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
-  using S = Shape<D>;
-  using X = Xch<D>;
-  __shared__ float xres[D], xs[D], x2s[D], os[D], hs[4 * D];
-  __shared__ float part[256];
-  __shared__ float red[16];
-  __shared__ float qkvs[192];  // this head's q, new k, new v
-  __shared__ float wm[NW], wl[NW], wo[NW][64];
-  __shared__ float aph[AC * 68];  // the head's attention partials (last arriver only)
-  __shared__ int last_s;
-  __shared__ float bias_s[2][32];  // this block's qkv, proj, fc, mproj bias slices, by layer parity
+  using S = Shape<D, H>;
+  using U = Xu<D>;
+  using XL = Xl<D, H>;
+  constexpr int KC = S::KC, KC4 = S::KC4;
+  __shared__ __align__(16) float xres[D];
+  __shared__ __align__(16) float x2s[D];
+  __shared__ __align__(16) float os[D];
+  __shared__ __align__(16) float hs[4 * D];
+  __shared__ __align__(16) float qkvs[192];      // this head's q, new k, new v
+  __shared__ __align__(16) float pw[NDW][KPW];   // softmax numerators per data wave
+  __shared__ __align__(16) float wo[NW][64];
+  __shared__ float wm[NW], wl[NW];
+  __shared__ __align__(16) float aph[S::SPH][PART];  // partials of the head's other blocks (combiner)
+  __shared__ float bias_s[2][S::BT];
+  __shared__ float hval[S::RMAX];
   __shared__ int fail_s;
 
   const int blk = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const bool ctrl = w == NW - 1;
+  // The dispatcher deals consecutive blocks to consecutive XCDs, continuing
+  // from wherever the previous dispatch stopped: the XCD comes from the
+  // hardware, and blocks b = 8k .. 8k+7 (slot k) land on 8 different XCDs.
+  const int xcd = (int)xcc_id() & (NX - 1), slot = blk / NX;
+  // the QKV columns depend on (XCD, slot): their tiles and biases are stored
+  // under the virtual block id vb; everything else is indexed by blk
+  const int vb = slot * NX + xcd;
   if (tid == 0) fail_s = 0;
   const unsigned tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
   trace_mark(p.trace, 0);
 
   const int n = *p.src.step;
-  const int pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token
+  const int pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token (>= 1)
   int tokid = p.src.tokens[p.src.tok_off + n];
   if ((unsigned)tokid >= (unsigned)p.V) tokid = 0;
-  const int H = p.H, ctx = p.ctx;
-  const NcBuf nc(p.pairs, p.uc_bytes);
-  const bool attn_blk = blk < H * AC;
-  const int ah = blk / AC, achunk = blk % AC;
-  const int nk = pos + 1, per = (nk + AC - 1) / AC;
-  const int j0 = min(nk, achunk * per), j1 = min(nk, j0 + per);
-  const int kpw = (j1 - j0 + NDW - 1) / NDW;
-  const int a0 = min(j1, j0 + w * kpw), a1 = min(j1, a0 + kpw);  // this data wave's keys
+  const int ctx = p.ctx;
+  uint2* const xl = p.xl + (size_t)xcd * XL::STRIDE;  // this XCD's local pairs
+  const int xl0 = xcd * XL::STRIDE;                   // same, as a pair index into p.xl
 
-  float4 rq[S::QMAX], rp[S::PMAX], rf[S::FMAX], rm[S::MMAX];
-  float l1w[S::PER], l1b[S::PER], l2w[S::PER], l2b[S::PER];
-  float kreg[KG], vreg[KG];
-  tile_load<S::QMAX, S::QCH>(rq, p.tiles + (size_t)blk * S::QT);
-  load_ln<D>(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B, l1w, l1b);
+  // qkv columns: the XCD's heads h = xcd + 8j (j < nh) own columns
+  // [j*192, j*192+192) of the XCD's list (q, k, v of each head); slot s has qc of them
+  const int nh = (H - xcd + NX - 1) / NX;
+  const int qc = 3 * S::HD * nh / SLOTS, qcw = qc / NDW;
+  // attention role: local head hj = slot / SPH, key block kb = slot % SPH
+  const int hj = slot / S::SPH, kb = slot % S::SPH;
+  const int ah = xcd + NX * hj;
+  const int nk = pos + 1, nkb = (nk + KPB - 1) / KPB;
+  const bool attn_blk = hj < nh && kb < nkb;
 
   // x = tok_emb[id] + pos_emb[pos] (every block keeps its own copy)
   for (int i = tid; i < D; i += NT) xres[i] = p.tok[(size_t)tokid * D + i] + p.pos[(size_t)pos * D + i];
-  __syncthreads();
 
+  // The control wave and the data waves run separate loops that meet at the
+  // same sequence of barriers; each barrier that follows a wait is followed
+  // by a check of fail_s in both loops.
   bool ok = true;
-  auto fail = [&]() { fail_s = 1; };
-#define SYNC_OK()       \
-  __syncthreads();      \
-  if (fail_s) {         \
-    ok = false;         \
-    break;              \
+#define SYNC_OK()  \
+  __syncthreads(); \
+  if (fail_s) {    \
+    ok = false;    \
+    break;         \
   }
+  if (ctrl) {
+    // ================= control wave: collects every hand-off =================
+    const NcBuf ncu(p.uc, p.uc_bytes), ncl(p.xl, p.xl_bytes);
 #define TM(i) \
   if (l == 1) trace_mark(p.trace, 128 + (i))
-  for (int l = 0; l < p.L; l++) {
-    const unsigned tA = tagbase + 5 * l, tB = tA + 1, tC = tA + 2, tD = tA + 3, tE = tA + 4;
-    const float* vl = p.vecs + (size_t)l * S::VL;
-    const float* tl = p.tiles + (size_t)l * S::LAYER;
-    const float* t_proj = tl + (size_t)NB * S::QT + (size_t)blk * S::PT;
-    const float* t_fc = tl + (size_t)NB * (S::QT + S::PT) + (size_t)blk * S::FT;
-    const float* t_mp = tl + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)blk * S::MT;
-    const int ln = min(l + 1, p.L - 1);
-    const float* t_qkv_next = p.tiles + (size_t)ln * S::LAYER + (size_t)blk * S::QT;
-    const float* vnext = p.vecs + (size_t)ln * S::VL;
-    const float* Kc = p.kc + ((size_t)l * H + ah) * ctx * 64;
-    const float* Vc = p.vc + ((size_t)l * H + ah) * ctx * 64;
-
-    // ---- A: LN1 + QKV ----
-    if (ctrl) {
-      constexpr int NBIAS = S::QCOL + 2 * S::PCOL + S::FCOL;
-      if (lane < NBIAS) {
-        int off;
-        if (lane < S::QCOL) off = S::V_QKVB + blk * S::QCOL + lane;
-        else if (lane < S::QCOL + S::PCOL) off = S::V_PROJB + blk * S::PCOL + (lane - S::QCOL);
-        else if (lane < S::QCOL + S::PCOL + S::FCOL) off = S::V_FCB + blk * S::FCOL + (lane - S::QCOL - S::PCOL);
-        else off = S::V_MPB + blk * S::PCOL + (lane - S::QCOL - S::PCOL - S::FCOL);
-        bias_s[l & 1][lane] = vl[off];
-      }
-    }
-    load_ln<D>(vl + S::V_LN2W, vl + S::V_LN2B, l2w, l2b);
-    if (l > 0 && ctrl && !wait_pairs<D>(nc, X::X, tagbase + 5 * (l - 1) + 4, xres, p.err)) fail();
-    SYNC_OK();
-    TM(0);
-    layernorm_regs<D>(xres, xs, l1w, l1b, red);
-    tile_dot<S::QMAX, S::QCH, S::KC>(rq, xs, part);
-    tile_load<S::PMAX, S::PCH>(rp, t_proj);
-    __syncthreads();
-    TM(1);
-    if (tid < S::QCOL) {
-      const int col = blk * S::QCOL + tid;
-      float s = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < S::KC; kc++) s += part[tid * S::KC + kc];
-      s += bias_s[l & 1][tid];
-      put_pair(p.pairs + X::QKV + col, s, tA);
-      if (col >= D) {  // new K or V row of this position, for later steps
-        const int c = col - D, isv = c >= D, cc = isv ? c - D : c, h = cc >> 6, e = cc & 63;
-        (isv ? p.vc : p.kc)[(((size_t)l * H + h) * ctx + pos) * 64 + e] = s;
-      }
-    }
-
-    // ---- B: attention (head ah, key chunk achunk) ----
-    if (attn_blk) {
-      // cached K/V rows of the first key group do not depend on this step: the
-      // data waves request them while the control wave waits for q, k, v
-      if (!ctrl) {
-#pragma unroll
-        for (int i = 0; i < KG; i++) {
-          const int j = min(min(a0 + i, max(a0, a1 - 1)), pos);  // in bounds; row pos is replaced
-          kreg[i] = Kc[(size_t)j * 64 + lane];
-          vreg[i] = Vc[(size_t)j * 64 + lane];
-        }
-      }
-      if (ctrl) {
-        // q, k, v of this head: pairs [h*64, h*64+64) in each of the three thirds
-        long it = 0;
-        uint4 v0, v1, v2;
-        for (;;) {
-          reload_fence();
-          v0 = nc.load4((X::QKV + 0 * D + ah * 64) * 8 + (lane % 32) * 16);
-          v1 = nc.load4((X::QKV + 1 * D + ah * 64) * 8 + (lane % 32) * 16);
-          v2 = nc.load4((X::QKV + 2 * D + ah * 64) * 8 + (lane % 32) * 16);
-          const bool okk = v0.y == tA && v0.w == tA && v1.y == tA && v1.w == tA && v2.y == tA && v2.w == tA;
-          if (__all(okk)) break;
-          if (++it > SPIN_LIMIT || err_set(p.err)) {
-            if (lane == 0) raise_err(p.err);
-            fail();
-            break;
-          }
-        }
-        if (lane < 32) {
-          qkvs[2 * lane] = __uint_as_float(v0.x);
-          qkvs[2 * lane + 1] = __uint_as_float(v0.z);
-          qkvs[64 + 2 * lane] = __uint_as_float(v1.x);
-          qkvs[64 + 2 * lane + 1] = __uint_as_float(v1.z);
-          qkvs[128 + 2 * lane] = __uint_as_float(v2.x);
-          qkvs[128 + 2 * lane + 1] = __uint_as_float(v2.z);
-        }
-      }
+    for (int l = 0; l < p.L; l++) {
+      const unsigned tb = tagbase + PH * l;
+      const unsigned tA = tb, tP = tb + 1, tB = tb + 2, tC = tb + 3, tD = tb + 4;
+      // ---- A ----
+      if (lane < S::BT) bias_s[l & 1][lane] = p.btab[((size_t)l * NB + (lane < S::B_P ? vb : blk)) * S::BT + lane];
+      if (l > 0 && !gather<D>(ncu, U::X, tb - PH + 5, xres, p.err, err_code(W_X, l))) fail_s = 1;
       SYNC_OK();
-      TM(2);
-      if (!ctrl) {
-        // lane = head dim; this wave's keys a0..a1 in groups of KG (row pos from qkvs)
-        const float q = qkvs[lane];
-        float m = -INFINITY, lsum = 0.f, acc = 0.f;
-        for (int g0 = a0; g0 < a1; g0 += KG) {
-          if (g0 != a0) {
-#pragma unroll
-            for (int i = 0; i < KG; i++) {
-              const int j = min(min(g0 + i, a1 - 1), pos);
-              kreg[i] = Kc[(size_t)j * 64 + lane];
-              vreg[i] = Vc[(size_t)j * 64 + lane];
-            }
-          }
-          float sc[KG];
-          float gm = -INFINITY;
-#pragma unroll
-          for (int i = 0; i < KG; i++) {
-            const int j = g0 + i;
-            const float kv = (j == pos) ? qkvs[64 + lane] : kreg[i];
-            const float sv = wave_sum_dpp(q * kv) * 0.125f;
-            sc[i] = (j < a1) ? sv : -INFINITY;
-            gm = fmaxf(gm, sc[i]);
-          }
-          const float nm = fmaxf(m, gm);
-          const float corr = (m == -INFINITY) ? 0.f : expf(m - nm);
-          lsum *= corr;
-          acc *= corr;
-#pragma unroll
-          for (int i = 0; i < KG; i++) {
-            const int j = g0 + i;
-            const float pj = (j < a1) ? expf(sc[i] - nm) : 0.f;
-            lsum += pj;
-            acc += pj * ((j == pos) ? qkvs[128 + lane] : vreg[i]);
-          }
-          m = nm;
-        }
-        if (lane == 0) {
-          wm[w] = m;
-          wl[w] = lsum;
-        }
-        wo[w][lane] = acc;
-      } else {
-        if (lane == 0) {
-          wm[NW - 1] = -INFINITY;
-          wl[NW - 1] = 0.f;
-        }
-        wo[NW - 1][lane] = 0.f;
-      }
-      __syncthreads();
-      if (tid < 64) {
+      TM(0);
+      // ---- B ----
+      if (attn_blk) {
+        if (!gather<192>(ncl, xl0 + XL::QKV + hj * 192, tA, qkvs, p.err, err_code(W_QKV, l))) fail_s = 1;
+        SYNC_OK();
+        TM(2);
+        __syncthreads();  // the data waves' partials are in wm / wl / wo
         float M = -INFINITY;
-        for (int i = 0; i < NW; i++) M = fmaxf(M, wm[i]);
+#pragma unroll
+        for (int i = 0; i < NDW; i++) M = fmaxf(M, wm[i]);
         float Ls = 0.f, o = 0.f;
-        if (M != -INFINITY) {
-          for (int i = 0; i < NW; i++) {
-            const float f = (wm[i] == -INFINITY) ? 0.f : expf(wm[i] - M);
-            Ls += wl[i] * f;
-            o += wo[i][tid] * f;
+#pragma unroll
+        for (int i = 0; i < NDW; i++) {
+          const float f = (wm[i] == -INFINITY) ? 0.f : expf(wm[i] - M);
+          Ls += wl[i] * f;
+          o += wo[i][lane] * f;
+        }
+        if (nkb == 1) {
+          put_pair(p.uc + U::O + ah * 64 + lane, o / Ls, tB);
+        } else if (kb > 0) {
+          uint2* pp = xl + XL::PARTS + (hj * S::SPH + kb) * PART;
+          put_pair(pp + lane, o, tP);
+          if (lane < PART - 64) put_pair(pp + 64 + lane, lane == 0 ? M : (lane == 1 ? Ls : 0.f), tP);
+        } else {
+          // combiner: the head's other key blocks' partials
+          constexpr int Q = PART / 2;  // 16-byte loads per partial
+          constexpr int RM = ((S::SPH - 1) * Q + 63) / 64;
+          const int nload = (nkb - 1) * Q;
+          const int pbase = (xl0 + XL::PARTS + hj * S::SPH * PART + PART) * 8;  // partial kb = 1
+          uint4 v[RM];
+          long it = 0;
+          bool good = true;
+          for (;;) {
+            reload_fence();
+#pragma unroll
+            for (int r = 0; r < RM; r++) v[r] = ncl.load4(pbase + (r * 64 + lane) * 16);
+            bool okk = true;
+#pragma unroll
+            for (int r = 0; r < RM; r++)
+              if (r * 64 + lane < nload) okk &= (v[r].y == tP) & (v[r].w == tP);
+            if (__all(okk)) break;
+            if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+              if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_PART, l));
+              good = false;
+              break;
+            }
+          }
+          if (good) {
+            float* a = &aph[0][0];
+#pragma unroll
+            for (int r = 0; r < RM; r++) {
+              const int q = r * 64 + lane;
+              if (q < nload)
+                *reinterpret_cast<float2*>(a + 2 * q) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+            }
+            wave_lds_sync();
+            float M2 = M;
+            for (int c = 0; c < nkb - 1; c++) M2 = fmaxf(M2, aph[c][64]);
+            float f = expf(M - M2);
+            float L2 = Ls * f, o2 = o * f;
+            for (int c = 0; c < nkb - 1; c++) {
+              f = expf(aph[c][64] - M2);
+              L2 += aph[c][65] * f;
+              o2 += aph[c][lane] * f;
+            }
+            put_pair(p.uc + U::O + ah * 64 + lane, o2 / L2, tB);
+          } else {
+            fail_s = 1;
           }
         }
-        float* ap = p.apart + (size_t)blk * X::AP_STRIDE;
-        ap[tid] = o;
-        if (tid == 0) {
-          ap[64] = M;
-          ap[65] = Ls;
-        }
-        stores_done();
       }
-      __syncthreads();
-      // the last of the head's AC chunk blocks to arrive combines the partials
-      // and publishes the head's 64 outputs as tagged pairs
-      if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(p.hcnt + ah, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_s = (old % AC) == AC - 1;
-      }
-      __syncthreads();
-      if (last_s) {
-        reload_fence();
-        uint4* h4 = reinterpret_cast<uint4*>(aph);
-        for (int i = tid; i < AC * X::AP_STRIDE / 4; i += NT)
-          h4[i] = nc.load4(p.off_apart + (ah * AC * X::AP_STRIDE / 4 + i) * 16);
-        __syncthreads();
-        if (tid < 64) {
-          float M = -INFINITY;
-#pragma unroll
-          for (int c = 0; c < AC; c++) M = fmaxf(M, aph[c * X::AP_STRIDE + 64]);
-          float Ls = 0.f, o = 0.f;
-#pragma unroll
-          for (int c = 0; c < AC; c++) {
-            const float mc = aph[c * X::AP_STRIDE + 64];
-            const float f = (mc == -INFINITY) ? 0.f : expf(mc - M);
-            Ls += aph[c * X::AP_STRIDE + 65] * f;
-            o += aph[c * X::AP_STRIDE + tid] * f;
-          }
-          put_pair(p.pairs + X::O + ah * 64 + tid, o / Ls, tB);
-        }
-      }
+      TM(3);
+      // ---- C ----
+      if (!gather<D>(ncu, U::O, tB, os, p.err, err_code(W_O, l))) fail_s = 1;
+      SYNC_OK();
+      TM(4);
+      // ---- D ----
+      if (!gather<D>(ncu, U::X2, tC, x2s, p.err, err_code(W_X2, l))) fail_s = 1;
+      SYNC_OK();
+      TM(5);
+      // ---- E ----
+      if (!gather<4 * D>(ncu, U::HH, tD, hs, p.err, err_code(W_H, l))) fail_s = 1;
+      SYNC_OK();
+      TM(6);
     }
-    tile_load<S::FMAX, S::FCH>(rf, t_fc);
-
-    // ---- C: attn.proj + residual -> x2 ----
-    if (ctrl && !wait_pairs<D>(nc, X::O, tB, os, p.err)) fail();
-    SYNC_OK();
-    __syncthreads();
-    TM(3);
-    tile_dot<S::PMAX, S::PCH, S::KC>(rp, os, part);
-    tile_load<S::MMAX, S::MCH>(rm, t_mp);
-    __syncthreads();
-    if (tid < S::PCOL) {
-      const int col = blk * S::PCOL + tid;
-      float s = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < S::KC; kc++) s += part[tid * S::KC + kc];
-      put_pair(p.pairs + X::X2 + col, (s + bias_s[l & 1][S::QCOL + tid]) + xres[col], tC);
-    }
-
-    // ---- D: LN2 + mlp.fc + GELU -> h ----
-    if (ctrl && !wait_pairs<D>(nc, X::X2, tC, x2s, p.err)) fail();
-    SYNC_OK();
-    TM(4);
-    layernorm_regs<D>(x2s, xs, l2w, l2b, red);
-    tile_dot<S::FMAX, S::FCH, S::KC>(rf, xs, part);
-    tile_load<S::QMAX, S::QCH>(rq, t_qkv_next);
-    load_ln<D>(vnext + S::V_LN1W, vnext + S::V_LN1B, l1w, l1b);
-    __syncthreads();
-    if (tid < S::FCOL) {
-      const int col = blk * S::FCOL + tid;
-      float s = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < S::KC; kc++) s += part[tid * S::KC + kc];
-      put_pair(p.pairs + X::HH + col, gelu_tanh(s + bias_s[l & 1][S::QCOL + S::PCOL + tid]), tD);
-    }
-
-    // ---- E: mlp.proj + residual -> x ----
-    if (ctrl && !wait_pairs<4 * D>(nc, X::HH, tD, hs, p.err)) fail();
-    SYNC_OK();
-    TM(5);
-    tile_dot<S::MMAX, S::MCH, S::KC4>(rm, hs, part);
-    __syncthreads();
-    if (tid < S::PCOL) {
-      const int col = blk * S::PCOL + tid;
-      float s = 0.f;
-#pragma unroll
-      for (int kc = 0; kc < S::KC4; kc++) s += part[tid * S::KC4 + kc];
-      put_pair(p.pairs + X::X + col, (s + bias_s[l & 1][S::QCOL + S::PCOL + S::FCOL + tid]) + x2s[col], tE);
-    }
-    TM(6);
-  }
 #undef TM
-
-  if (ok) {
-    // ---- head: LN_f + tied projection over this block's vocab rows ----
-    const unsigned tH = tagbase + 5 * p.L;
-    const int R = p.V / NB;
-    const int nch = R * S::KC;
-    constexpr int HG = 8;  // head chunks per wave in flight
-    const float4* t4 = reinterpret_cast<const float4*>(p.tok + (size_t)blk * R * D);
-    float4 rh[HG];
-    if (w < NDW) {
-#pragma unroll
-      for (int i = 0; i < HG; i++) rh[i] = t4[min(w + NDW * i, nch - 1) * 64 + lane];
-    }
-    const float* vf = p.vecs + (size_t)p.L * S::VL;
-    load_ln<D>(vf, vf + D, l1w, l1b);
-    if (ctrl && !wait_pairs<D>(nc, X::X, tagbase + 5 * (p.L - 1) + 4, xres, p.err)) fail();
-    __syncthreads();
-    ok = !fail_s;
     if (ok) {
-      layernorm_regs<D>(xres, xs, l1w, l1b, red);
-      if (w < NDW) {
-        for (int g = 0; g < S::HMAX; g += HG) {
-          float4 nx[HG];
+      // ---- head ----
+      if (!gather<D>(ncu, U::X, tagbase + PH * (p.L - 1) + 5, xres, p.err, err_code(W_XF, 0))) fail_s = 1;
+      __syncthreads();
+      ok = !fail_s;
+      if (ok) {
+        __syncthreads();  // hval holds this block's logits
+        // block 0 collects every block's argmax: it proves all blocks read this
+        // launch's counter, so the counter can advance
+        const unsigned tH = tagbase + PH * p.L;
+        if (blk == 0) {
+          float best = -INFINITY;
+          int bi = 0x7fffffff;
+          long it = 0;
+          bool good = true;
+          for (;;) {
+            reload_fence();
+            bool okk = true;
+            best = -INFINITY;
+            bi = 0x7fffffff;
 #pragma unroll
-          for (int i = 0; i < HG; i++) nx[i] = t4[min(w + NDW * (g + HG + i), nch - 1) * 64 + lane];
-#pragma unroll
-          for (int i = 0; i < HG; i++) {
-            const int ch = w + NDW * (g + i);
-            if (ch < nch) {
-              const int kc = ch % S::KC;
-              const float4 xv = *reinterpret_cast<const float4*>(xs + kc * 256 + lane * 4);
-              const float q = wave_sum_dpp(rh[i].x * xv.x + rh[i].y * xv.y + rh[i].z * xv.z + rh[i].w * xv.w);
-              if (lane == 0) part[ch] = q;
+            for (int r = 0; r < NB / 64; r++) {
+              const uint4 a = ncu.load4(p.off_amax + 16 * (r * 64 + lane));
+              okk &= a.z == tH;
+              argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
+            }
+            if (__all(okk)) break;
+            if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+              if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_AMAX, 0));
+              good = false;
+              break;
             }
           }
-#pragma unroll
-          for (int i = 0; i < HG; i++) rh[i] = nx[i];
+          if (good) {
+            wave_argmax(best, bi);
+            if (lane == 0) {
+              if (p.greedy) {
+                const int total = p.src.tok_off + 1 + n;  // prompt_len + n
+                p.tokens_out[total] = bi;
+                if (n < p.max_new) p.out_ids[n] = bi;
+                if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+                *p.step_out = n + 1;
+              }
+              __hip_atomic_fetch_add(p.launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
         }
+      }
+    }
+  } else {
+    // ================= data waves: weights in registers =================
+    const int key0 = kb * KPB + w * KPW;  // this data wave's first key
+    const bool wave_keys = attn_blk && key0 < nk;
+    const int lpos = pos - key0;          // index of the new row within this wave's keys
+    // Register tiles, each requested two phases before its use; every load is
+    // unconditional (an empty buffer resource when there is nothing to fetch),
+    // so no register stays live across the whole layer loop:
+    //   after A: rf(l), LN2(l)   after B: rm(l)   after C: rq(l+1)
+    //   after D: LN1(l+1)        after E: rp(l+1), K/V(l+1)
+    float4 rq[S::QCW * KC], rp[KC], rf[S::FCW * KC], rm[KC4];
+    float4 kr[8];   // half a K row (dims 32*(lane/32) ..) of key key0 + lane % 32
+    float vr[KPW];  // V[key0 + i][lane]
+    float4 lnw[KC], lnb[KC];  // this lane's LayerNorm parameters: LN1(l) until A, LN2(l) until D
+    auto load_ln = [&](const float* wv, const float* bv) {
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(wv, D * 4), rb = make_rsrc(bv, D * 4);
+#pragma unroll
+      for (int c = 0; c < KC; c++) {
+        lnw[c] = ld4(rw, c * 1024 + lane * 16);
+        lnb[c] = ld4(rb, c * 1024 + lane * 16);
+      }
+    };
+    // a block with qcw < QCW columns per wave reads its chunks twice (same
+    // addresses, no extra HBM bytes) so the loads stay unconditional
+    auto load_q = [&](const float* tile, bool real) {
+      constexpr int HALF = S::QCW * KC / 2;
+      const __amdgpu_buffer_rsrc_t lo = make_rsrc(tile, real ? HALF * 1024 : 0);
+      const __amdgpu_buffer_rsrc_t hi = make_rsrc(qcw == S::QCW ? tile + HALF * 256 : tile, real ? HALF * 1024 : 0);
+      const int off = lane * 16;
+#pragma unroll
+      for (int i = 0; i < HALF; i++) rq[i] = ld4(lo, off + i * 1024);
+#pragma unroll
+      for (int i = 0; i < HALF; i++) rq[HALF + i] = ld4(hi, off + i * 1024);
+    };
+    static_assert(S::QCW % 2 == 0, "qkv chunks split in halves");
+    auto tile_q = [&](int l) { return p.tiles + (size_t)l * S::LAYER + (size_t)vb * S::QT + (size_t)w * qcw * D; };
+    auto tile_p = [&](int l) {
+      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * S::QT + (size_t)blk * S::PT + (size_t)w * D;
+    };
+    auto tile_f = [&](int l) {
+      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * (S::QT + S::PT) + (size_t)blk * S::FT +
+             (size_t)w * S::FCW * D;
+    };
+    auto tile_m = [&](int l) {
+      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)blk * S::MT +
+             (size_t)w * 4 * D;
+    };
+    // cached K/V rows of this wave's keys in layer l, through buffer resources
+    // bounded by the head's ctx rows (rows at or past the new one are masked
+    // below; nothing is fetched when real == false)
+    auto load_kv = [&](int l, bool real) {
+      const size_t hoff = ((size_t)l * H + ah) * ctx * 64;
+      const int bytes = real ? ctx * 256 : 0;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + (real ? hoff : 0), bytes);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + (real ? hoff : 0), bytes);
+      const int koff = (key0 + (lane & 31)) * 256 + 128 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 8; i++) kr[i] = ld4(rk, koff + 16 * i);
+      const int voff = key0 * 256 + lane * 4;
+#pragma unroll
+      for (int i = 0; i < KPW; i++)
+        vr[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, voff + 256 * i, 0, 0));
+    };
+    load_ln(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B);
+    load_q(tile_q(0), true);
+    load_chunks(rp, tile_p(0), true);
+    load_kv(0, wave_keys);
+
+    for (int l = 0; l < p.L; l++) {
+      const unsigned tb = tagbase + PH * l;
+      const unsigned tA = tb, tC = tb + 3, tD = tb + 4, tE = tb + 5;
+      const bool more = l + 1 < p.L;
+      const float* vl = p.vecs + (size_t)l * S::VL;
+      const float* vn = p.vecs + (size_t)(l + 1) * S::VL;  // next layer's (or ln_f after the last)
+      // ---- A: LN1 + QKV ----
+      SYNC_OK();
+      {
+        float4 xn[KC];
+        ln_lane<KC, D>(xres, lnw, lnb, xn);
+        float val = 0.f;
+#pragma unroll
+        for (int t = 0; t < S::QCW; t++) {
+          if (t < qcw) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < KC; c++) acc += dot4(rq[t * KC + c], xn[c]);
+            const float v = wave_sum_dpp(acc);
+            if (lane == t) val = v;
+          }
+        }
+        if (lane < qcw) {
+          const int i = slot * qc + w * qcw + lane;  // index in the XCD's column list
+          const float s = val + bias_s[l & 1][S::B_Q + w * qcw + lane];
+          put_pair(xl + XL::QKV + i, s, tA);
+          const int j = i / 192, r = i % 192, part = r / 64, e = r % 64;
+          if (part > 0) {  // new K or V row of this position, for later steps
+            const int h = xcd + NX * j;
+            (part == 2 ? p.vc : p.kc)[(((size_t)l * H + h) * ctx + pos) * 64 + e] = s;
+          }
+        }
+        // prefetches go after the output: a wave with many loads in flight can stall at issue
+        load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
+        load_chunks(rf, tile_f(l), true);
+      }
+      // ---- B: attention of head ah over key block kb ----
+      if (attn_blk) {
+        SYNC_OK();
+        if (wave_keys) {
+          // scores: lanes l and l + 32 hold halves of key key0 + l's row
+          const int half = lane >> 5, kl = lane & 31;
+          float sacc = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; i++) {
+            const float4 q4 = *reinterpret_cast<const float4*>(qkvs + 32 * half + 4 * i);
+            const float4 k4 = (kl == lpos) ? *reinterpret_cast<const float4*>(qkvs + 64 + 32 * half + 4 * i) : kr[i];
+            sacc += dot4(q4, k4);
+          }
+          sacc += __shfl_xor(sacc, 32, 64);
+          const bool valid = key0 + kl < nk;
+          const float sc = valid ? sacc * 0.125f : -INFINITY;
+          const float mw = wave_max_dpp(sc);
+          const float pj = (valid && half == 0) ? expf(sc - mw) : 0.f;
+          const float lw = wave_sum_dpp(pj);
+          if (half == 0) pw[w][kl] = pj;
+          wave_lds_sync();
+          // P.V: lane = dim; rows past the new one may hold anything (even NaN),
+          // so they are never multiplied
+          const float vnew = qkvs[128 + lane];
+          float oacc = 0.f;
+#pragma unroll
+          for (int i = 0; i < KPW / 4; i++) {
+            const float4 p4 = *reinterpret_cast<const float4*>(&pw[w][4 * i]);
+            oacc += p4.x * ((4 * i + 0 < lpos) ? vr[4 * i + 0] : (4 * i + 0 == lpos ? vnew : 0.f));
+            oacc += p4.y * ((4 * i + 1 < lpos) ? vr[4 * i + 1] : (4 * i + 1 == lpos ? vnew : 0.f));
+            oacc += p4.z * ((4 * i + 2 < lpos) ? vr[4 * i + 2] : (4 * i + 2 == lpos ? vnew : 0.f));
+            oacc += p4.w * ((4 * i + 3 < lpos) ? vr[4 * i + 3] : (4 * i + 3 == lpos ? vnew : 0.f));
+          }
+          if (lane == 0) {
+            wm[w] = mw;
+            wl[w] = lw;
+          }
+          wo[w][lane] = oacc;
+        } else {
+          if (lane == 0) {
+            wm[w] = -INFINITY;
+            wl[w] = 0.f;
+          }
+          wo[w][lane] = 0.f;
+        }
+        __syncthreads();
+      }
+      load_chunks(rm, tile_m(l), true);
+      // ---- C: attn.proj + residual -> x2 ----
+      SYNC_OK();
+      {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC; c++) acc += dot4(rp[c], *reinterpret_cast<const float4*>(os + c * 256 + lane * 4));
+        const float v = wave_sum_dpp(acc);
+        if (lane == 0) {
+          const int col = blk * S::PCOL + w;
+          put_pair(p.uc + U::X2 + col, (v + bias_s[l & 1][S::B_P + w]) + xres[col], tC);
+        }
+        load_q(tile_q(more ? l + 1 : l), more);
+      }
+      // ---- D: LN2 + mlp.fc + GELU -> h ----
+      SYNC_OK();
+      {
+        float4 xn[KC];
+        ln_lane<KC, D>(x2s, lnw, lnb, xn);
+        float val = 0.f;
+#pragma unroll
+        for (int t = 0; t < S::FCW; t++) {
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < KC; c++) acc += dot4(rf[t * KC + c], xn[c]);
+          const float v = wave_sum_dpp(acc);
+          if (lane == t) val = v;
+        }
+        if (lane < S::FCW) {
+          const int c = w * S::FCW + lane;
+          put_pair(p.uc + U::HH + blk * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
+        }
+        load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
+      }
+      // ---- E: mlp.proj + residual -> x ----
+      SYNC_OK();
+      {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < KC4; c++) acc += dot4(rm[c], *reinterpret_cast<const float4*>(hs + c * 256 + lane * 4));
+        const float v = wave_sum_dpp(acc);
+        if (lane == 0) {
+          const int col = blk * S::PCOL + w;
+          put_pair(p.uc + U::X + col, (v + bias_s[l & 1][S::B_M + w]) + x2s[col], tE);
+        }
+        load_chunks(rp, tile_p(more ? l + 1 : l), more);
+        load_kv(more ? l + 1 : l, more && wave_keys);
+      }
+    }
+    if (ok) {
+      // ---- head: LN_f + tied projection over this block's vocab rows ----
+      const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
+      constexpr int HG = 4;    // rows per wave in flight
+      const float* E = p.tok + (size_t)blk * R * D;
+      float4 rh[HG * KC];
+      const int nrow = (R - w + NDW - 1) / NDW;  // rows of this wave
+#pragma unroll
+      for (int t = 0; t < HG; t++) {
+        const int row = w + NDW * min(t, nrow - 1);
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+          rh[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
       }
       __syncthreads();
-      if (w == 0) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        if (lane < R) {
-          float s = 0.f;
+      ok = !fail_s;
+      if (ok) {
+        float4 xn[KC];
+        ln_lane<KC, D>(xres, lnw, lnb, xn);
+        for (int g = 0; g < nrow; g += HG) {
+          float4 nx[HG * KC];
 #pragma unroll
-          for (int kc = 0; kc < S::KC; kc++) s += part[lane * S::KC + kc];
-          const int v = blk * R + lane;
-          p.logits[v] = s;
-          best = s;
-          bi = v;
-        }
-        wave_argmax(best, bi);
-        if (lane == 0) {  // value and index first, tag last
-          *reinterpret_cast<uint2*>(&p.amax[blk]) = make_uint2(__float_as_uint(best), (unsigned)bi);
-          stores_done();
-          reinterpret_cast<unsigned*>(&p.amax[blk])[2] = tH;
-        }
-      }
-      // block 0 collects every block's argmax: it proves all blocks read this
-      // launch's counter, so the counter can advance
-      if (blk == 0 && ctrl) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        long it = 0;
-        bool good = true;
-        for (;;) {
-          reload_fence();
-          bool okk = true;
-          best = -INFINITY;
-          bi = 0x7fffffff;
-          for (int b = lane; b < NB; b += 64) {
-            const uint4 a = nc.load4(p.off_amax + 16 * b);
-            okk &= a.z == tH;
-            argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
+          for (int t = 0; t < HG; t++) {
+            const int row = w + NDW * min(g + HG + t, nrow - 1);
+#pragma unroll
+            for (int c = 0; c < KC; c++)
+              nx[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
           }
-          if (__all(okk)) break;
-          if (++it > SPIN_LIMIT || err_set(p.err)) {
-            if (lane == 0) raise_err(p.err);
-            good = false;
-            break;
-          }
-        }
-        if (good) {
-          wave_argmax(best, bi);
-          if (lane == 0) {
-            if (p.greedy) {
-              const int total = p.src.tok_off + 1 + n;  // prompt_len + n
-              p.tokens_out[total] = bi;
-              if (n < p.max_new) p.out_ids[n] = bi;
-              if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
-              *p.step_out = n + 1;
+#pragma unroll
+          for (int t = 0; t < HG; t++) {
+            if (g + t < nrow) {
+              float acc = 0.f;
+#pragma unroll
+              for (int c = 0; c < KC; c++) acc += dot4(rh[t * KC + c], xn[c]);
+              const float v = wave_sum_dpp(acc);
+              if (lane == 0) hval[w + NDW * (g + t)] = v;
             }
-            __hip_atomic_fetch_add(p.launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
+#pragma unroll
+          for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
+        }
+        __syncthreads();
+        if (w == 0) {
+          const unsigned tH = tagbase + PH * p.L;
+          float best = -INFINITY;
+          int bi = 0x7fffffff;
+          if (lane < R) {
+            const float s = hval[lane];
+            const int v = blk * R + lane;
+            p.logits[v] = s;
+            best = s;
+            bi = v;
+          }
+          wave_argmax(best, bi);
+          if (lane == 0)
+            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * blk) =
+                make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
         }
       }
     }
   }
-  (void)fail;
+#undef SYNC_OK
   trace_mark(p.trace, 127);
 }
 
-// tile[b][c][k] = W[k][b*ncol + c] for a row-major W [K][N]
-__global__ void k_relayout(const float* __restrict__ W, int K, int N, int ncol, float* __restrict__ tile) {
+__global__ void k_xcc_probe(unsigned* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
+// tile[b][c][k] = W[k][map[b*ncol + c]] (0 where map < 0), W row-major [K][N]
+__global__ void k_relayout(const float* __restrict__ W, int K, int N, const int* __restrict__ map, int ncol,
+                           float* __restrict__ tile) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (size_t)K * N) return;
+  if (i >= (size_t)NB * ncol * K) return;
   const int k = (int)(i % K);
   const size_t bc = i / K;
-  const int c = (int)(bc % ncol), b = (int)(bc / ncol);
-  tile[i] = W[(size_t)k * N + (size_t)b * ncol + c];
+  const int col = map[bc];
+  tile[i] = col >= 0 ? W[(size_t)k * N + col] : 0.f;
+}
+
+// out[b*32 + j] = src[map[b*ncol + j]] for j < ncol (one bias slice of the table)
+__global__ void k_gather_bias(const float* __restrict__ src, const int* __restrict__ map, int ncol, int off,
+                              float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= NB * ncol) return;
+  const int b = i / ncol, j = i % ncol, col = map[i];
+  out[b * 32 + off + j] = col >= 0 ? src[col] : 0.f;
 }
 
 __global__ void k_copy(const float* __restrict__ src, float* __restrict__ dst, int n) {
@@ -701,16 +803,32 @@ void uc_give(int dev, size_t bytes, void* p) {
   g_uc_free.emplace_back(dev, bytes, p);
 }
 
-// uncached region layout (bytes)
-struct UcLayout {
-  size_t pairs, apart, amax, total;
-  UcLayout(int D, int H) {
-    pairs = 0;
-    apart = pairs + (size_t)10 * D * sizeof(uint2);
-    amax = (apart + (size_t)H * AC * 68 * sizeof(float) + 255) / 256 * 256;
-    total = amax + (size_t)NB * sizeof(uint4);
+constexpr int kD = 768, kH = 12;
+using S768 = Shape<kD, kH>;
+
+size_t uc_pairs_bytes(int D) { return (size_t)Xu<kD>::NPAIR * sizeof(uint2) * (D / kD); }
+size_t uc_total_bytes(int D) { return (uc_pairs_bytes(D) + 255) / 256 * 256 + (size_t)NB * sizeof(uint4); }
+
+// column maps (host): qkv by XCD head ownership, stored under the virtual block
+// id b = slot * 8 + XCD; the others contiguous per block
+void make_maps(int D, int H, std::vector<int>& q, std::vector<int>& pr, std::vector<int>& fc) {
+  using S = S768;
+  q.assign((size_t)NB * S::QCMAX, -1);
+  for (int b = 0; b < NB; b++) {
+    const int x = b % NX, s = b / NX;
+    const int nh = (H - x + NX - 1) / NX;
+    const int qc = 3 * 64 * nh / SLOTS;
+    for (int c = 0; c < qc; c++) {
+      const int i = s * qc + c, j = i / 192, r = i % 192, part = r / 64, e = r % 64;
+      const int h = x + NX * j;
+      q[(size_t)b * S::QCMAX + c] = part * D + h * 64 + e;
+    }
   }
-};
+  pr.resize((size_t)NB * S::PCOL);
+  for (int i = 0; i < NB * S::PCOL; i++) pr[i] = i;
+  fc.resize((size_t)NB * S::FCOL);
+  for (int i = 0; i < NB * S::FCOL; i++) fc[i] = i;
+}
 
 }  // namespace
 
@@ -721,25 +839,43 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   L = d.n_layers;
   V = d.vocab_size;
   ctx = d.context_length;
-  C = AC;
+  C = KPB;
   blocks = NB;
-  const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == 768 && D / H == 64 && V % NB == 0 &&
-                        V / NB <= 64 && H * AC <= 192 && H * AC <= NB && compute_units >= NB &&
-                        5 * L + 2 <= TAGS;
+  const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == kD && H == kH && V % NB == 0 &&
+                        V / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH && compute_units >= NB &&
+                        PH * L + 1 <= TAGS;
   if (!shape_ok) return FH_OK;
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<768>, NT, 0) != hipSuccess || occ < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH>, NT, 0) != hipSuccess || occ < 1)
     return FH_OK;
   if (hipGetDevice(&device) != hipSuccess) return FH_ERR_HIP;
-  tile_floats = (size_t)12 * D * D * L;
+  {
+    // the XCD-local hand-offs need 8 XCDs dealt blocks round-robin (blocks
+    // 8k .. 8k+7 on distinct XCDs); keep the generic path otherwise
+    unsigned* dx = nullptr;
+    std::vector<unsigned> hx(NB);
+    if (hipMalloc(&dx, NB * sizeof(unsigned)) != hipSuccess) return FH_ERR_OOM;
+    hipLaunchKernelGGL(k_xcc_probe, dim3(NB), dim3(64), 0, 0, dx);
+    const bool got = hipGetLastError() == hipSuccess &&
+                     hipMemcpy(hx.data(), dx, NB * sizeof(unsigned), hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(dx);
+    if (!got) return FH_ERR_HIP;
+    for (int b = 0; b < NB; b++)
+      if (hx[b] >= (unsigned)NX || hx[b] != (hx[0] + b) % NX) return FH_OK;
+  }
+  tile_floats = S768::LAYER * L;
   if (hipMalloc(&tiles, tile_floats * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
-  const size_t vec_floats = (size_t)13 * D * L + 2 * D;
+  const size_t vec_floats = (size_t)S768::VL * L + 2 * D;
   if (hipMalloc(&vecs, vec_floats * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
-  UcLayout u(D, H);
-  xch_bytes = u.total;
+  if (hipMalloc(&btab, (size_t)L * NB * S768::BT * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
+  xch_bytes = uc_total_bytes(D);
   uc = static_cast<char*>(uc_take(device, xch_bytes));
   if (!uc) return FH_ERR_OOM;
+  xl_bytes = (size_t)NX * Xl<kD, kH>::STRIDE * sizeof(uint2);
+  if (hipMalloc(&xl, xl_bytes) != hipSuccess) return FH_ERR_OOM;
   if (hipMalloc(&ctl, 256) != hipSuccess) return FH_ERR_OOM;
+  if (hipMemset(ctl, 0, 256) != hipSuccess) return FH_ERR_HIP;
+  counter = 1;
   if (reset_state() != FH_OK) return FH_ERR_HIP;
   const char* tr = getenv("FORGE_HIP_TRACE");
   if (tr && tr[0] == '1') {
@@ -752,41 +888,55 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
 
 int FastDecode::build(hipStream_t st, const float* const* params) {
   if (!enabled) return FH_OK;
-  const int qcol = 3 * D / NB, pcol = D / NB, fcol = 4 * D / NB;
+  using S = S768;
+  std::vector<int> qm, pm, fm;
+  make_maps(D, H, qm, pm, fm);
+  int* dmap = nullptr;
+  const size_t nmap = qm.size() + pm.size() + fm.size();
+  if (hipMalloc(&dmap, nmap * sizeof(int)) != hipSuccess) return FH_ERR_OOM;
+  int* dq = dmap;
+  int* dp = dq + qm.size();
+  int* df = dp + pm.size();
+  int rc = FH_OK;
   auto copy = [&](const float* src, float* dst, int n) {
     hipLaunchKernelGGL(k_copy, dim3((n + 255) / 256), dim3(256), 0, st, src, dst, n);
     return hipGetLastError() == hipSuccess;
   };
-  for (int l = 0; l < L; l++) {
-    float* tl = tiles + (size_t)l * 12 * D * D;
+  auto relayout = [&](const float* W, int K, int N, const int* map, int ncol, float* out) {
+    const size_t tot = (size_t)NB * ncol * K;
+    hipLaunchKernelGGL(k_relayout, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, W, K, N, map, ncol, out);
+    return hipGetLastError() == hipSuccess;
+  };
+  auto bias = [&](const float* src, const int* map, int ncol, int off, float* out) {
+    hipLaunchKernelGGL(k_gather_bias, dim3((NB * ncol + 255) / 256), dim3(256), 0, st, src, map, ncol, off, out);
+    return hipGetLastError() == hipSuccess;
+  };
+  if (hipMemcpy(dq, qm.data(), qm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dp, pm.data(), pm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(df, fm.data(), fm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+    rc = FH_ERR_HIP;
+  for (int l = 0; l < L && rc == FH_OK; l++) {
+    float* tl = tiles + (size_t)l * S::LAYER;
     const float* const* PL = params + 2 + 12 * l;
-    struct {
-      const float* W;
-      int K, N, ncol;
-      float* out;
-    } jobs[4] = {
-        {PL[2], D, 3 * D, qcol, tl},
-        {PL[4], D, D, pcol, tl + (size_t)3 * D * D},
-        {PL[8], D, 4 * D, fcol, tl + (size_t)4 * D * D},
-        {PL[10], 4 * D, D, pcol, tl + (size_t)8 * D * D},
-    };
-    for (auto& j : jobs) {
-      const size_t tot = (size_t)j.K * j.N;
-      hipLaunchKernelGGL(k_relayout, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, j.W, j.K, j.N, j.ncol,
-                         j.out);
-      if (hipGetLastError() != hipSuccess) return FH_ERR_HIP;
-    }
-    float* vl = vecs + (size_t)l * 13 * D;
-    // ln1.w ln1.b qkv.b proj.b ln2.w ln2.b fc.b mproj.b (registry slots 0,1,3,5,6,7,9,11)
-    if (!copy(PL[0], vl, D) || !copy(PL[1], vl + D, D) || !copy(PL[3], vl + 2 * D, 3 * D) ||
-        !copy(PL[5], vl + 5 * D, D) || !copy(PL[6], vl + 6 * D, D) || !copy(PL[7], vl + 7 * D, D) ||
-        !copy(PL[9], vl + 8 * D, 4 * D) || !copy(PL[11], vl + 12 * D, D))
-      return FH_ERR_HIP;
+    float* bt = btab + (size_t)l * NB * S::BT;
+    // registry slots: 0 ln1.w 1 ln1.b 2 qkv.w 3 qkv.b 4 proj.w 5 proj.b 6 ln2.w 7 ln2.b 8 fc.w 9 fc.b 10 mproj.w 11 mproj.b
+    const bool good = relayout(PL[2], D, 3 * D, dq, S::QCMAX, tl) &&
+                      relayout(PL[4], D, D, dp, S::PCOL, tl + (size_t)NB * S::QT) &&
+                      relayout(PL[8], D, 4 * D, df, S::FCOL, tl + (size_t)NB * (S::QT + S::PT)) &&
+                      relayout(PL[10], 4 * D, D, dp, S::PCOL, tl + (size_t)NB * (S::QT + S::PT + S::FT)) &&
+                      bias(PL[3], dq, S::QCMAX, S::B_Q, bt) && bias(PL[5], dp, S::PCOL, S::B_P, bt) &&
+                      bias(PL[9], df, S::FCOL, S::B_F, bt) && bias(PL[11], dp, S::PCOL, S::B_M, bt);
+    float* vl = vecs + (size_t)l * S::VL;
+    if (!good || !copy(PL[0], vl + S::V_LN1W, D) || !copy(PL[1], vl + S::V_LN1B, D) ||
+        !copy(PL[6], vl + S::V_LN2W, D) || !copy(PL[7], vl + S::V_LN2B, D))
+      rc = FH_ERR_HIP;
   }
   const float* const* PF = params + 2 + 12 * L;
-  if (!copy(PF[0], vecs + (size_t)13 * D * L, D) || !copy(PF[1], vecs + (size_t)13 * D * L + D, D))
-    return FH_ERR_HIP;
-  return hipStreamSynchronize(st) == hipSuccess ? FH_OK : FH_ERR_HIP;
+  if (rc == FH_OK && (!copy(PF[0], vecs + (size_t)S::VL * L, D) || !copy(PF[1], vecs + (size_t)S::VL * L + D, D)))
+    rc = FH_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) rc = FH_ERR_HIP;
+  (void)hipFree(dmap);
+  return rc;
 }
 
 int FastDecode::enqueue(hipStream_t st, const Step& s) {
@@ -794,11 +944,11 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   if (!s.src.tokens || !s.src.step || !s.tokens || !s.step || !s.kcache || !s.vcache || !s.logits || !s.out_ids ||
       !s.out_counts || s.src.pos_mul != 1 || s.max_new <= 0)
     return FH_ERR_INVALID;
-  UcLayout u(D, H);
   KParams k{};
   k.src = s.src;
   k.tiles = tiles;
   k.vecs = vecs;
+  k.btab = btab;
   k.tok = s.tok_emb;
   k.pos = s.pos_emb;
   k.kc = s.kcache;
@@ -806,18 +956,15 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.logits = s.logits;
   k.out_ids = s.out_ids;
   k.out_counts = s.out_counts;
-  k.pairs = reinterpret_cast<uint2*>(uc + u.pairs);
-  k.apart = reinterpret_cast<float*>(uc + u.apart);
-  k.hcnt = reinterpret_cast<unsigned*>(ctl) + 32;
-  k.amax = reinterpret_cast<uint4*>(uc + u.amax);
-  k.uc_bytes = (int)u.total;
-  k.off_apart = (int)u.apart;
-  k.off_amax = (int)u.amax;
+  k.uc = reinterpret_cast<uint2*>(uc);
+  k.uc_bytes = (int)xch_bytes;
+  k.off_amax = (int)((uc_pairs_bytes(D) + 255) / 256 * 256);
+  k.xl = reinterpret_cast<uint2*>(xl);
+  k.xl_bytes = (int)xl_bytes;
   k.launch = reinterpret_cast<unsigned*>(ctl);
   k.err = reinterpret_cast<int*>(ctl) + 16;
   k.V = V;
   k.ctx = ctx;
-  k.H = H;
   k.L = L;
   k.max_new = s.max_new;
   k.eos = s.eos;
@@ -825,37 +972,59 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.tokens_out = s.tokens;
   k.step_out = s.step;
   k.trace = trace;
-  hipLaunchKernelGGL(k_decode_step<768>, dim3(NB), dim3(NT), 0, st, k);
+  hipLaunchKernelGGL((k_decode_step<kD, kH>), dim3(NB), dim3(NT), 0, st, k);
   return hipGetLastError() == hipSuccess ? FH_OK : FH_ERR_HIP;
 }
 
-// Tags of zeroed memory are 0; the launch counter starts at 1, so no live tag
-// (counter * 128 + phase) ever equals a stale or cleared one.
+int FastDecode::before_launches(int n) {
+  if (!enabled || n <= 0) return FH_OK;
+  // keep launch counter * 128 far from wrapping in 32 bits
+  if (launched + (unsigned long long)n >= (1ull << 24)) {
+    launched = 0;
+    counter = 1;
+    return reset_state();
+  }
+  launched += (unsigned long long)n;
+  return FH_OK;
+}
+
+// The launch counter starts at `counter`; every launch advances it by one.  A
+// reset continues past every value a failed launch may have used, so no live
+// tag (counter * 128 + phase) ever equals a stale one, and zeroed memory (tag
+// 0) never matches either.
 int FastDecode::reset_state() {
-  const unsigned one = 1;
+  unsigned cur = 0;
+  if (ctl && hipMemcpy(&cur, ctl, sizeof cur, hipMemcpyDeviceToHost) != hipSuccess) return FH_ERR_HIP;
+  if (cur + 2 > counter) counter = cur + 2;
   if (hipMemset(ctl, 0, 256) != hipSuccess) return FH_ERR_HIP;
-  if (hipMemcpy(ctl, &one, sizeof one, hipMemcpyHostToDevice) != hipSuccess) return FH_ERR_HIP;
+  if (hipMemcpy(ctl, &counter, sizeof counter, hipMemcpyHostToDevice) != hipSuccess) return FH_ERR_HIP;
   if (hipMemset(uc, 0, xch_bytes) != hipSuccess) return FH_ERR_HIP;
+  if (hipMemset(xl, 0, xl_bytes) != hipSuccess) return FH_ERR_HIP;
   return hipDeviceSynchronize() == hipSuccess ? FH_OK : FH_ERR_HIP;
 }
 
 int FastDecode::reset() { return enabled ? reset_state() : FH_OK; }
 
-int FastDecode::check_error() {
+int FastDecode::check_error(unsigned* code) {
+  if (code) *code = 0;
   if (!enabled) return FH_OK;
-  int h = 0;
-  if (hipMemcpy(&h, reinterpret_cast<int*>(ctl) + 16, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess)
+  unsigned h = 0;
+  if (hipMemcpy(&h, reinterpret_cast<int*>(ctl) + 16, sizeof h, hipMemcpyDeviceToHost) != hipSuccess)
     return FH_ERR_HIP;
+  if (code) *code = h;
   return h ? FH_ERR_HIP : FH_OK;
 }
 
 void FastDecode::release() {
   if (tiles) (void)hipFree(tiles);
   if (vecs) (void)hipFree(vecs);
+  if (btab) (void)hipFree(btab);
+  if (xl) (void)hipFree(xl);
   uc_give(device, xch_bytes, uc);
   if (ctl) (void)hipFree(ctl);
   if (trace) (void)hipFree(trace);
-  tiles = vecs = nullptr;
+  tiles = vecs = btab = nullptr;
+  xl = nullptr;
   uc = nullptr;
   ctl = nullptr;
   trace = nullptr;

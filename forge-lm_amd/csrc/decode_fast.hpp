@@ -17,10 +17,15 @@ struct FastDecode {
   int blocks = 0;
   int device = 0;
   float* tiles = nullptr;            // per-block weight tiles, column-major
-  float* vecs = nullptr;             // LayerNorm parameters and biases at fixed offsets
-  char* uc = nullptr;                // uncached hand-off area (pairs, attention partials, argmax)
+  float* vecs = nullptr;             // LayerNorm parameters at fixed offsets
+  float* btab = nullptr;             // per-layer, per-block bias slices
+  char* uc = nullptr;                // uncached hand-off area (cross-XCD pairs, argmax records)
   size_t xch_bytes = 0;
-  void* ctl = nullptr;  // launch counter (word 0), error word (16), per-head arrival counters (32..)
+  void* xl = nullptr;                // per-XCD hand-off area (q/k/v, attention partials)
+  size_t xl_bytes = 0;
+  void* ctl = nullptr;  // launch counter (word 0), error word (16)
+  unsigned counter = 1;                 // launch counter value set at the last reset
+  unsigned long long launched = 0;      // launches since that reset
   unsigned long long* trace = nullptr;  // timestamps of the last step (FORGE_HIP_TRACE=1)
   size_t tile_floats = 0;
 
@@ -43,7 +48,12 @@ struct FastDecode {
     int* step;
   };
   int enqueue(hipStream_t st, const Step& s);
-  int check_error();
+  // Called before n more launches (graph replays included); resets the tag
+  // state before the launch counter could wrap.
+  int before_launches(int n);
+  // FH_ERR_HIP when a wait of the last launches gave up; *code (optional)
+  // says which: 1 << 31 | wait << 24 | layer << 16 | block.
+  int check_error(unsigned* code = nullptr);
   int reset();  // fresh launch counter, cleared hand-off area and error word
   void release();
 

@@ -862,6 +862,8 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   // which of steps 1..max_new-1 are cached decode steps (window fits) vs re-prefills
   int n_dec = 0, n_re = 0;
   for (int n = 1; n < max_new; n++) (P + n > C ? n_re : n_dec)++;
+  if (s->use_fast() && n_dec > 0 && s->fast.before_launches(n_dec) != FH_OK)
+    return set_err(FH_ERR_HIP, "resetting the fused decode state failed");
   if (n_dec > 0) {
     GraphKey k = key;
     k.kind = 0;
@@ -893,9 +895,13 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   if (logits_dump)
     HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * max_new * V, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
-  if (s->use_fast() && n_dec > 0 && s->fast.check_error() != FH_OK) {
+  unsigned wait_code = 0;
+  if (s->use_fast() && n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
     s->fast.reset();
-    return set_err(FH_ERR_HIP, "fused decode step: a grid barrier wait exceeded its spin limit (results discarded)");
+    return set_err(FH_ERR_HIP,
+                   "fused decode step: a hand-off wait exceeded its spin limit (wait %u, layer %u, block %u; "
+                   "results discarded)",
+                   (wait_code >> 24) & 0x7f, (wait_code >> 16) & 0xff, wait_code & 0xffff);
   }
   for (int b = 0; b < B; b++)
     if (out_counts[b] < 0) out_counts[b] = max_new;
