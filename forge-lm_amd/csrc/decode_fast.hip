@@ -181,6 +181,10 @@ struct KParams {
 __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
   if (t && blockIdx.x == 0 && threadIdx.x == (NT - 64) && i < 256) t[i] = wall_clock64();
 }
+// same, from data wave 0
+__device__ __forceinline__ void trace_mark_d(unsigned long long* t, int i) {
+  if (t && blockIdx.x == 0 && threadIdx.x == 0 && i < 256) t[i] = wall_clock64();
+}
 
 // Control wave: waits until pairs[pair0, pair0 + N) all carry `tag`, then
 // stores the values to out[0, N) (LDS).  One read in flight: a second poll
@@ -214,6 +218,15 @@ __device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int
       *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
   }
   return true;
+}
+
+// sum over the 16 lanes of each DPP row (quad permutes, half-row and row mirrors)
+__device__ __forceinline__ float row16_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
 }
 
 __device__ __forceinline__ float dot4(const float4 a, const float4 b) {
@@ -283,7 +296,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   __shared__ __align__(16) float os[D];
   __shared__ __align__(16) float hs[4 * D];
   __shared__ __align__(16) float qkvs[192];      // this head's q, new k, new v
-  __shared__ __align__(16) float pw[NDW][KPW];   // softmax numerators per data wave
   __shared__ __align__(16) float wo[NW][64];
   __shared__ float wm[NW], wl[NW];
   __shared__ __align__(16) float aph[S::SPH][PART];  // partials of the head's other blocks (combiner)
@@ -291,7 +303,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   __shared__ float hval[S::RMAX];
   __shared__ int fail_s;
 
-  const int blk = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  // w is wave-uniform; readfirstlane lets the compiler know, so buffer
+  // resources built from it stay in scalar registers
+  const int blk = blockIdx.x, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const bool ctrl = w == NW - 1;
   // The dispatcher deals consecutive blocks to consecutive XCDs, continuing
   // from wherever the previous dispatch stopped: the XCD comes from the
@@ -337,6 +351,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   }
   if (ctrl) {
     // ================= control wave: collects every hand-off =================
+    // its polls are issued ahead of the data waves' queued bulk loads
+    __builtin_amdgcn_s_setprio(3);
     const NcBuf ncu(p.uc, p.uc_bytes), ncl(p.xl, p.xl_bytes);
 #define TM(i) \
   if (l == 1) trace_mark(p.trace, 128 + (i))
@@ -486,15 +502,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     // ================= data waves: weights in registers =================
     const int key0 = kb * KPB + w * KPW;  // this data wave's first key
     const bool wave_keys = attn_blk && key0 < nk;
-    const int lpos = pos - key0;          // index of the new row within this wave's keys
     // Register tiles, each requested two phases before its use; every load is
     // unconditional (an empty buffer resource when there is nothing to fetch),
     // so no register stays live across the whole layer loop:
     //   after A: rf(l), LN2(l)   after B: rm(l)   after C: rq(l+1)
     //   after D: LN1(l+1)        after E: rp(l+1), K/V(l+1)
     float4 rq[S::QCW * KC], rp[KC], rf[S::FCW * KC], rm[KC4];
-    float4 kr[8];   // half a K row (dims 32*(lane/32) ..) of key key0 + lane % 32
-    float vr[KPW];  // V[key0 + i][lane]
+    // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
+    // lane l the dims 4*(l % 16) .. +3 of row key0 + 4i + l / 16 (one 1 KB load each)
+    float4 kr[KPW / 4], vr[KPW / 4];
     float4 lnw[KC], lnb[KC];  // this lane's LayerNorm parameters: LN1(l) until A, LN2(l) until D
     auto load_ln = [&](const float* wv, const float* bv) {
       const __amdgpu_buffer_rsrc_t rw = make_rsrc(wv, D * 4), rb = make_rsrc(bv, D * 4);
@@ -537,14 +553,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       const int bytes = real ? ctx * 256 : 0;
       const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + (real ? hoff : 0), bytes);
       const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + (real ? hoff : 0), bytes);
-      const int koff = (key0 + (lane & 31)) * 256 + 128 * (lane >> 5);
+      const int off = key0 * 256 + lane * 16;
 #pragma unroll
-      for (int i = 0; i < 8; i++) kr[i] = ld4(rk, koff + 16 * i);
-      const int voff = key0 * 256 + lane * 4;
+      for (int i = 0; i < KPW / 4; i++) kr[i] = ld4(rk, off + 1024 * i);
 #pragma unroll
-      for (int i = 0; i < KPW; i++)
-        vr[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rv, voff + 256 * i, 0, 0));
+      for (int i = 0; i < KPW / 4; i++) vr[i] = ld4(rv, off + 1024 * i);
     };
+#define TD(i) \
+  if (l == 1) trace_mark_d(p.trace, 160 + (i))
     load_ln(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B);
     load_q(tile_q(0), true);
     load_chunks(rp, tile_p(0), true);
@@ -558,9 +574,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       const float* vn = p.vecs + (size_t)(l + 1) * S::VL;  // next layer's (or ln_f after the last)
       // ---- A: LN1 + QKV ----
       SYNC_OK();
+      TD(0);
       {
         float4 xn[KC];
         ln_lane<KC, D>(xres, lnw, lnb, xn);
+        TD(1);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::QCW; t++) {
@@ -582,48 +600,62 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
             (part == 2 ? p.vc : p.kc)[(((size_t)l * H + h) * ctx + pos) * 64 + e] = s;
           }
         }
+        TD(2);
         // prefetches go after the output: a wave with many loads in flight can stall at issue
         load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
         load_chunks(rf, tile_f(l), true);
+        TD(3);
       }
       // ---- B: attention of head ah over key block kb ----
       if (attn_blk) {
         SYNC_OK();
+        TD(12);
         if (wave_keys) {
-          // scores: lanes l and l + 32 hold halves of key key0 + l's row
-          const int half = lane >> 5, kl = lane & 31;
-          float sacc = 0.f;
-#pragma unroll
-          for (int i = 0; i < 8; i++) {
-            const float4 q4 = *reinterpret_cast<const float4*>(qkvs + 32 * half + 4 * i);
-            const float4 k4 = (kl == lpos) ? *reinterpret_cast<const float4*>(qkvs + 64 + 32 * half + 4 * i) : kr[i];
-            sacc += dot4(q4, k4);
-          }
-          sacc += __shfl_xor(sacc, 32, 64);
-          const bool valid = key0 + kl < nk;
-          const float sc = valid ? sacc * 0.125f : -INFINITY;
-          const float mw = wave_max_dpp(sc);
-          const float pj = (valid && half == 0) ? expf(sc - mw) : 0.f;
-          const float lw = wave_sum_dpp(pj);
-          if (half == 0) pw[w][kl] = pj;
-          wave_lds_sync();
-          // P.V: lane = dim; rows past the new one may hold anything (even NaN),
-          // so they are never multiplied
-          const float vnew = qkvs[128 + lane];
-          float oacc = 0.f;
+          // lane l: dims 4*(l % 16) .. +3 of keys key0 + 4i + l / 16, i < KPW / 4
+          const int g = lane >> 4, d4 = 4 * (lane & 15);
+          const float4 q4 = *reinterpret_cast<const float4*>(qkvs + d4);
+          const float4 knew = *reinterpret_cast<const float4*>(qkvs + 64 + d4);
+          const float4 vnew = *reinterpret_cast<const float4*>(qkvs + 128 + d4);
+          float sc[KPW / 4];
+          float mloc = -INFINITY;
 #pragma unroll
           for (int i = 0; i < KPW / 4; i++) {
-            const float4 p4 = *reinterpret_cast<const float4*>(&pw[w][4 * i]);
-            oacc += p4.x * ((4 * i + 0 < lpos) ? vr[4 * i + 0] : (4 * i + 0 == lpos ? vnew : 0.f));
-            oacc += p4.y * ((4 * i + 1 < lpos) ? vr[4 * i + 1] : (4 * i + 1 == lpos ? vnew : 0.f));
-            oacc += p4.z * ((4 * i + 2 < lpos) ? vr[4 * i + 2] : (4 * i + 2 == lpos ? vnew : 0.f));
-            oacc += p4.w * ((4 * i + 3 < lpos) ? vr[4 * i + 3] : (4 * i + 3 == lpos ? vnew : 0.f));
+            const int j = key0 + 4 * i + g;
+            float sp = dot4(q4, j == pos ? knew : kr[i]);
+            sp = row16_sum(sp);  // all 16 lanes of the row now hold key j's q.k
+            sc[i] = j < nk ? sp * 0.125f : -INFINITY;
+            mloc = fmaxf(mloc, sc[i]);
+          }
+          const float mw = wave_max_dpp(mloc);
+          float lloc = 0.f;
+          float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+          for (int i = 0; i < KPW / 4; i++) {
+            const int j = key0 + 4 * i + g;
+            const float pj = j < nk ? expf(sc[i] - mw) : 0.f;
+            lloc += pj;
+            // rows past the new one may hold anything (even NaN): never multiplied
+            const float4 v = j < pos ? vr[i] : (j == pos ? vnew : make_float4(0.f, 0.f, 0.f, 0.f));
+            o4.x += pj * v.x;
+            o4.y += pj * v.y;
+            o4.z += pj * v.z;
+            o4.w += pj * v.w;
+          }
+          const float lw = wave_sum_dpp((lane & 15) == 0 ? lloc : 0.f);
+          // sum the four key groups (lanes l, l^16, l^32, l^48)
+#pragma unroll
+          for (int m = 16; m <= 32; m *= 2) {
+            o4.x += __shfl_xor(o4.x, m, 64);
+            o4.y += __shfl_xor(o4.y, m, 64);
+            o4.z += __shfl_xor(o4.z, m, 64);
+            o4.w += __shfl_xor(o4.w, m, 64);
           }
           if (lane == 0) {
             wm[w] = mw;
             wl[w] = lw;
           }
-          wo[w][lane] = oacc;
+          if (g == 0) *reinterpret_cast<float4*>(&wo[w][d4]) = o4;
+          TD(13);
         } else {
           if (lane == 0) {
             wm[w] = -INFINITY;
@@ -636,6 +668,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       load_chunks(rm, tile_m(l), true);
       // ---- C: attn.proj + residual -> x2 ----
       SYNC_OK();
+      TD(4);
       {
         float acc = 0.f;
 #pragma unroll
@@ -645,13 +678,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           const int col = blk * S::PCOL + w;
           put_pair(p.uc + U::X2 + col, (v + bias_s[l & 1][S::B_P + w]) + xres[col], tC);
         }
+        TD(5);
         load_q(tile_q(more ? l + 1 : l), more);
       }
       // ---- D: LN2 + mlp.fc + GELU -> h ----
       SYNC_OK();
+      TD(6);
       {
         float4 xn[KC];
         ln_lane<KC, D>(x2s, lnw, lnb, xn);
+        TD(7);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::FCW; t++) {
@@ -665,10 +701,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           const int c = w * S::FCW + lane;
           put_pair(p.uc + U::HH + blk * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
         }
+        TD(8);
         load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
       }
       // ---- E: mlp.proj + residual -> x ----
       SYNC_OK();
+      TD(9);
       {
         float acc = 0.f;
 #pragma unroll
@@ -678,10 +716,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           const int col = blk * S::PCOL + w;
           put_pair(p.uc + U::X + col, (v + bias_s[l & 1][S::B_M + w]) + x2s[col], tE);
         }
+        TD(10);
         load_chunks(rp, tile_p(more ? l + 1 : l), more);
         load_kv(more ? l + 1 : l, more && wave_keys);
+        TD(11);
       }
     }
+#undef TD
     if (ok) {
       // ---- head: LN_f + tied projection over this block's vocab rows ----
       const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
