@@ -61,7 +61,7 @@ constexpr int SLOTS = NB / NX;
 constexpr int KPW = 32;            // attention keys per data wave (two lanes per key)
 constexpr int KPB = KPW * NDW;     // attention keys per block
 constexpr int TAGS = 128;          // tag values reserved per launch
-constexpr int PH = 6;              // tagged phases per layer
+constexpr int PH = 8;              // tagged phases per layer
 constexpr long SPIN_LIMIT = 400000;
 constexpr int PART = 68;           // pairs per attention partial: o[64], m, l, pad[2]
 
@@ -69,9 +69,10 @@ __device__ __forceinline__ bool err_set(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 // The first failing wait records where it was: 1 << 31 | wait << 24 | layer << 16 | block
-// (waits: 1 x, 2 q/k/v, 3 partials, 4 o, 5 x2, 6 h, 7 final x, 8 argmax).
+// (waits: 1 x, 2 q/k/v, 3 attention partials, 4 o, 5 attn.proj partials, 6 x2, 7 h,
+// 8 mlp.proj partials, 9 final x, 10 argmax).
 // A wait that gives up because another block already failed records nothing.
-enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_X2, W_H, W_XF, W_AMAX };
+enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX };
 __device__ __forceinline__ int err_code(int wait, int l) {
   return (int)(0x80000000u | ((unsigned)wait << 24) | ((unsigned)(l & 0xff) << 16) | blockIdx.x);
 }
@@ -116,41 +117,51 @@ struct NcBuf {
 template <int D, int H>
 struct Shape {
   static constexpr int HD = 64;
-  static constexpr int KC = D / 256;       // 256-float chunks per K=D column
-  static constexpr int KC4 = 4 * D / 256;  // chunks per K=4D column
+  static constexpr int KC = D / 256;             // 256-float chunks per K=D column
   static constexpr int HPX = (H + NX - 1) / NX;  // heads per XCD (at most)
   static constexpr int SPH = SLOTS / HPX;        // slots per head
   static constexpr int QCMAX = 3 * HD * HPX / SLOTS;  // qkv columns per block (at most)
   static constexpr int QCW = QCMAX / NDW;              // qkv columns per data wave (at most)
-  static constexpr int PCOL = D / NB;      // attn.proj / mlp.proj columns per block (one per data wave)
-  static constexpr int FCOL = 4 * D / NB;  // mlp.fc columns per block
+  static constexpr int HX = 4 * D / NX;    // mlp.fc columns (h values) per XCD
+  static constexpr int FCOL = HX / SLOTS;  // h values per block
   static constexpr int FCW = FCOL / NDW;   // per data wave
+  static constexpr int RSC = D / SLOTS;    // output columns per slot of attn.proj / mlp.proj
+  static constexpr int G = RSC / NDW / 4;  // 4-column groups per data wave
+  static constexpr int PJ = HPX;           // attn.proj: one 64-row piece per head of the XCD
+  static constexpr int MJ = HX / 64;       // mlp.proj: 64-row pieces of the XCD's h slice
   static constexpr int RMAX = 64;          // vocab rows per block (V <= 16384)
-  // tile floats per block
-  static constexpr size_t QT = (size_t)QCMAX * D, PT = (size_t)PCOL * D, FT = (size_t)FCOL * D,
-                          MT = (size_t)PCOL * 4 * D;
+  // tile floats per (virtual) block; the 1 KB chunks of attn.proj / mlp.proj hold
+  // 4 output columns x 64 rows (lane l: rows 4*(l%16)..+3 of column l/16)
+  static constexpr size_t QT = (size_t)QCMAX * D, PT = (size_t)PJ * NDW * G * 256, FT = (size_t)FCOL * D,
+                          MT = (size_t)NDW * G * MJ * 256;
   static constexpr size_t LAYER = (size_t)NB * (QT + PT + FT + MT);
   // compact vector buffer per layer: ln1.w ln1.b ln2.w ln2.b
   static constexpr int V_LN1W = 0, V_LN1B = D, V_LN2W = 2 * D, V_LN2B = 3 * D, VL = 4 * D;
-  // per-block bias table per layer: qkv[QCMAX] proj[PCOL] fc[FCOL] mproj[PCOL]
-  static constexpr int B_Q = 0, B_P = QCMAX, B_F = QCMAX + PCOL, B_M = QCMAX + PCOL + FCOL, BT = 32;
+  // per-block bias table per layer: qkv[QCMAX] fc[FCOL] proj[RSC] mproj[RSC]
+  static constexpr int B_Q = 0, B_F = QCMAX, B_P = QCMAX + FCOL, B_M = QCMAX + FCOL + RSC,
+                       BT = QCMAX + FCOL + 2 * RSC;
   static_assert(D == H * HD, "head_dim 64");
-  static_assert(D % 256 == 0 && D % NB == 0 && PCOL == NDW, "one proj column per data wave");
-  static_assert(QCMAX % NDW == 0 && FCOL % NDW == 0, "columns split evenly over the data waves");
-  static_assert(B_M + PCOL <= BT, "bias table row");
+  static_assert(D % 256 == 0 && HX % SLOTS == 0 && HX % 64 == 0, "chunked columns");
+  static_assert(QCMAX % NDW == 0 && FCOL % NDW == 0 && RSC % (4 * NDW) == 0, "columns split evenly");
   static_assert(SPH * HPX == SLOTS, "slots split evenly over an XCD's heads");
 };
 
-// uncached (cross-XCD) pair layout
+// uncached (cross-XCD) pair layout: the per-XCD partial sums of attn.proj and mlp.proj
 template <int D>
 struct Xu {
-  static constexpr int X = 0, X2 = D, HH = 2 * D, O = 6 * D, NPAIR = 7 * D;
+  static constexpr int PX2 = 0, PX = NX * D, NPAIR = 2 * NX * D;
 };
-// per-XCD local pair layout: qkv of the XCD's heads, then the attention partials
+// per-XCD local pair layout
 template <int D, int H>
 struct Xl {
   using S = Shape<D, H>;
-  static constexpr int QKV = 0, PARTS = 3 * S::HD * S::HPX, STRIDE = PARTS + S::HPX * S::SPH * PART;
+  static constexpr int QKV = 0;                                   // q, k, v of the XCD's heads
+  static constexpr int PARTS = QKV + 3 * S::HD * S::HPX;          // attention partials
+  static constexpr int O = PARTS + S::HPX * S::SPH * PART;        // o of the XCD's heads
+  static constexpr int X2 = O + S::HD * S::HPX;                   // x2 (every XCD keeps a copy)
+  static constexpr int HH = X2 + D;                               // the XCD's h slice
+  static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
+  static constexpr int STRIDE = X + D;
 };
 
 struct KParams {
@@ -186,12 +197,12 @@ __device__ __forceinline__ void trace_mark_d(unsigned long long* t, int i) {
   if (t && blockIdx.x == 0 && threadIdx.x == 0 && i < 256) t[i] = wall_clock64();
 }
 
-// Control wave: waits until pairs[pair0, pair0 + N) all carry `tag`, then
-// stores the values to out[0, N) (LDS).  One read in flight: a second poll
+// Control wave: waits until pairs[pair0, pair0 + n) all carry `tag` (n <= N),
+// then stores the values to out[0, n) (LDS).  One read in flight: a second poll
 // issued ahead would still be in flight when the wait ends, and reusing its
 // registers would wait for it.
 template <int N>
-__device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int* err, int code) {
+__device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int* err, int code, int n = N) {
   static_assert(N % 2 == 0, "pairs come in 16-byte loads");
   constexpr int R = (N + 127) / 128;
   const int lane = threadIdx.x & 63;
@@ -204,7 +215,7 @@ __device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int
     bool ok = true;
 #pragma unroll
     for (int r = 0; r < R; r++)
-      if (N % 128 == 0 || (r * 64 + lane) * 2 < N) ok &= (v[r].y == tag) & (v[r].w == tag);
+      if ((r * 64 + lane) * 2 < n) ok &= (v[r].y == tag) & (v[r].w == tag);
     if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
       if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
@@ -214,8 +225,45 @@ __device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int i = 2 * (r * 64 + lane);
-    if (N % 128 == 0 || i < N)
-      *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+    if (i < n) *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+  }
+  return true;
+}
+
+// Control wave: the RSC-column slice [slot*RSC, +RSC) of all NX per-XCD partial
+// vectors (pairs at pair0 + x*D + c), into out[x*RSC + c] (LDS).
+template <int D, int RSC>
+__device__ bool gather_slices(const NcBuf& nc, int pair0, int slot, unsigned tag, float* out, int* err, int code) {
+  constexpr int Q = RSC / 2;  // 16-byte loads per slice
+  constexpr int NQ = NX * Q;
+  constexpr int R = (NQ + 63) / 64;
+  const int lane = threadIdx.x & 63;
+  uint4 v[R];
+  long it = 0;
+  for (;;) {
+    reload_fence();
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const int u = min(r * 64 + lane, NQ - 1), x = u / Q, q = u % Q;
+      v[r] = nc.load4((pair0 + x * D + slot * RSC + 2 * q) * 8);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int r = 0; r < R; r++) ok &= (v[r].y == tag) & (v[r].w == tag);
+    if (__all(ok)) break;
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
+      return false;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const int u = r * 64 + lane;
+    if (u < NQ) {
+      const int x = u / Q, q = u % Q;
+      *reinterpret_cast<float2*>(out + x * RSC + 2 * q) =
+          make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+    }
   }
   return true;
 }
@@ -290,12 +338,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   using S = Shape<D, H>;
   using U = Xu<D>;
   using XL = Xl<D, H>;
-  constexpr int KC = S::KC, KC4 = S::KC4;
+  constexpr int KC = S::KC, RSC = S::RSC, G = S::G;
   __shared__ __align__(16) float xres[D];
   __shared__ __align__(16) float x2s[D];
-  __shared__ __align__(16) float os[D];
-  __shared__ __align__(16) float hs[4 * D];
-  __shared__ __align__(16) float qkvs[192];      // this head's q, new k, new v
+  __shared__ __align__(16) float os[S::HD * S::HPX];  // o of the XCD's heads
+  __shared__ __align__(16) float hs[S::HX];           // the XCD's h slice
+  __shared__ __align__(16) float rsv[NX * RSC];       // this slot's columns of the per-XCD partials
+  __shared__ __align__(16) float qkvs[192];           // this head's q, new k, new v
   __shared__ __align__(16) float wo[NW][64];
   __shared__ float wm[NW], wl[NW];
   __shared__ __align__(16) float aph[S::SPH][PART];  // partials of the head's other blocks (combiner)
@@ -311,8 +360,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // from wherever the previous dispatch stopped: the XCD comes from the
   // hardware, and blocks b = 8k .. 8k+7 (slot k) land on 8 different XCDs.
   const int xcd = (int)xcc_id() & (NX - 1), slot = blk / NX;
-  // the QKV columns depend on (XCD, slot): their tiles and biases are stored
-  // under the virtual block id vb; everything else is indexed by blk
+  // every tile and bias depends on (XCD, slot): they are stored under the
+  // virtual block id vb; the head rows are indexed by blk
   const int vb = slot * NX + xcd;
   if (tid == 0) fail_s = 0;
   const unsigned tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
@@ -351,24 +400,23 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   }
   if (ctrl) {
     // ================= control wave: collects every hand-off =================
-    // its polls are issued ahead of the data waves' queued bulk loads
-    __builtin_amdgcn_s_setprio(3);
     const NcBuf ncu(p.uc, p.uc_bytes), ncl(p.xl, p.xl_bytes);
 #define TM(i) \
   if (l == 1) trace_mark(p.trace, 128 + (i))
     for (int l = 0; l < p.L; l++) {
       const unsigned tb = tagbase + PH * l;
-      const unsigned tA = tb, tP = tb + 1, tB = tb + 2, tC = tb + 3, tD = tb + 4;
-      // ---- A ----
-      if (lane < S::BT) bias_s[l & 1][lane] = p.btab[((size_t)l * NB + (lane < S::B_P ? vb : blk)) * S::BT + lane];
-      if (l > 0 && !gather<D>(ncu, U::X, tb - PH + 5, xres, p.err, err_code(W_X, l))) fail_s = 1;
+      const unsigned tA = tb, tP = tb + 1, tB = tb + 2, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6,
+                     tE2 = tb + 7;
+      // ---- A: x of this layer (every XCD's copy) ----
+      for (int i = lane; i < S::BT; i += 64) bias_s[l & 1][i] = p.btab[((size_t)l * NB + vb) * S::BT + i];
+      if (l > 0 && !gather<D>(ncl, xl0 + XL::X, tb - PH + 7, xres, p.err, err_code(W_X, l))) fail_s = 1;
       SYNC_OK();
       TM(0);
-      // ---- B ----
+      // ---- B: attention ----
       if (attn_blk) {
         if (!gather<192>(ncl, xl0 + XL::QKV + hj * 192, tA, qkvs, p.err, err_code(W_QKV, l))) fail_s = 1;
         SYNC_OK();
-        TM(2);
+        TM(1);
         __syncthreads();  // the data waves' partials are in wm / wl / wo
         float M = -INFINITY;
 #pragma unroll
@@ -381,7 +429,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           o += wo[i][lane] * f;
         }
         if (nkb == 1) {
-          put_pair(p.uc + U::O + ah * 64 + lane, o / Ls, tB);
+          put_pair(xl + XL::O + hj * 64 + lane, o / Ls, tB);
         } else if (kb > 0) {
           uint2* pp = xl + XL::PARTS + (hj * S::SPH + kb) * PART;
           put_pair(pp + lane, o, tP);
@@ -428,30 +476,50 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
               L2 += aph[c][65] * f;
               o2 += aph[c][lane] * f;
             }
-            put_pair(p.uc + U::O + ah * 64 + lane, o2 / L2, tB);
+            put_pair(xl + XL::O + hj * 64 + lane, o2 / L2, tB);
           } else {
             fail_s = 1;
           }
         }
       }
+      TM(2);
+      // ---- C: o of the XCD's heads ----
+      if (!gather<S::HD * S::HPX>(ncl, xl0 + XL::O, tB, os, p.err, err_code(W_O, l), S::HD * nh)) fail_s = 1;
+      SYNC_OK();
       TM(3);
-      // ---- C ----
-      if (!gather<D>(ncu, U::O, tB, os, p.err, err_code(W_O, l))) fail_s = 1;
+      // ---- x2 = x + attn.proj(o) + b: this slot's columns from the 8 XCD partials ----
+      if (!gather_slices<D, RSC>(ncu, U::PX2, slot, tC, rsv, p.err, err_code(W_PX2, l))) fail_s = 1;
+      wave_lds_sync();
+      if (lane < RSC) {
+        float sum = 0.f;
+#pragma unroll
+        for (int x = 0; x < NX; x++) sum += rsv[x * RSC + lane];
+        const int col = slot * RSC + lane;
+        put_pair(xl + XL::X2 + col, (sum + bias_s[l & 1][S::B_P + lane]) + xres[col], tC2);
+      }
+      if (!gather<D>(ncl, xl0 + XL::X2, tC2, x2s, p.err, err_code(W_X2, l))) fail_s = 1;
       SYNC_OK();
       TM(4);
-      // ---- D ----
-      if (!gather<D>(ncu, U::X2, tC, x2s, p.err, err_code(W_X2, l))) fail_s = 1;
+      // ---- D: the XCD's h slice ----
+      if (!gather<S::HX>(ncl, xl0 + XL::HH, tD, hs, p.err, err_code(W_H, l))) fail_s = 1;
       SYNC_OK();
       TM(5);
-      // ---- E ----
-      if (!gather<4 * D>(ncu, U::HH, tD, hs, p.err, err_code(W_H, l))) fail_s = 1;
-      SYNC_OK();
+      // ---- E: x = x2 + mlp.proj(h) + b: this slot's columns from the 8 XCD partials ----
+      if (!gather_slices<D, RSC>(ncu, U::PX, slot, tE, rsv, p.err, err_code(W_PX, l))) fail_s = 1;
+      wave_lds_sync();
+      if (lane < RSC) {
+        float sum = 0.f;
+#pragma unroll
+        for (int x = 0; x < NX; x++) sum += rsv[x * RSC + lane];
+        const int col = slot * RSC + lane;
+        put_pair(xl + XL::X + col, (sum + bias_s[l & 1][S::B_M + lane]) + x2s[col], tE2);
+      }
       TM(6);
     }
 #undef TM
     if (ok) {
       // ---- head ----
-      if (!gather<D>(ncu, U::X, tagbase + PH * (p.L - 1) + 5, xres, p.err, err_code(W_XF, 0))) fail_s = 1;
+      if (!gather<D>(ncl, xl0 + XL::X, tagbase + PH * (p.L - 1) + 7, xres, p.err, err_code(W_XF, 0))) fail_s = 1;
       __syncthreads();
       ok = !fail_s;
       if (ok) {
@@ -507,7 +575,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     // so no register stays live across the whole layer loop:
     //   after A: rf(l), LN2(l)   after B: rm(l)   after C: rq(l+1)
     //   after D: LN1(l+1)        after E: rp(l+1), K/V(l+1)
-    float4 rq[S::QCW * KC], rp[KC], rf[S::FCW * KC], rm[KC4];
+    float4 rq[S::QCW * KC], rp[S::PJ * G], rf[S::FCW * KC], rm[G * S::MJ];
     // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
     // lane l the dims 4*(l % 16) .. +3 of row key0 + 4i + l / 16 (one 1 KB load each)
     float4 kr[KPW / 4], vr[KPW / 4];
@@ -520,12 +588,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
         lnb[c] = ld4(rb, c * 1024 + lane * 16);
       }
     };
-    // a block with qcw < QCW columns per wave reads its chunks twice (same
+    auto tile = [&](int l) { return p.tiles + (size_t)l * S::LAYER; };
+    // qkv: a block with qcw < QCW columns per wave reads its chunks twice (same
     // addresses, no extra HBM bytes) so the loads stay unconditional
-    auto load_q = [&](const float* tile, bool real) {
+    auto load_q = [&](int l, bool real) {
       constexpr int HALF = S::QCW * KC / 2;
-      const __amdgpu_buffer_rsrc_t lo = make_rsrc(tile, real ? HALF * 1024 : 0);
-      const __amdgpu_buffer_rsrc_t hi = make_rsrc(qcw == S::QCW ? tile + HALF * 256 : tile, real ? HALF * 1024 : 0);
+      const float* t = tile(l) + (size_t)vb * S::QT + (size_t)w * qcw * D;
+      const __amdgpu_buffer_rsrc_t lo = make_rsrc(t, real ? HALF * 1024 : 0);
+      const __amdgpu_buffer_rsrc_t hi = make_rsrc(qcw == S::QCW ? t + HALF * 256 : t, real ? HALF * 1024 : 0);
       const int off = lane * 16;
 #pragma unroll
       for (int i = 0; i < HALF; i++) rq[i] = ld4(lo, off + i * 1024);
@@ -533,17 +603,24 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       for (int i = 0; i < HALF; i++) rq[HALF + i] = ld4(hi, off + i * 1024);
     };
     static_assert(S::QCW % 2 == 0, "qkv chunks split in halves");
-    auto tile_q = [&](int l) { return p.tiles + (size_t)l * S::LAYER + (size_t)vb * S::QT + (size_t)w * qcw * D; };
-    auto tile_p = [&](int l) {
-      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * S::QT + (size_t)blk * S::PT + (size_t)w * D;
+    // attn.proj chunks are ordered [head piece j][wave][group]: pieces past the
+    // XCD's head count lie outside the resource and read as zeros
+    auto load_p = [&](int l, bool real) {
+      const float* t = tile(l) + (size_t)NB * S::QT + (size_t)vb * S::PT;
+      const __amdgpu_buffer_rsrc_t rs = make_rsrc(t, real ? nh * NDW * G * 1024 : 0);
+#pragma unroll
+      for (int j = 0; j < S::PJ; j++)
+#pragma unroll
+        for (int g = 0; g < G; g++) rp[j * G + g] = ld4(rs, ((j * NDW + w) * G + g) * 1024 + lane * 16);
     };
-    auto tile_f = [&](int l) {
-      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * (S::QT + S::PT) + (size_t)blk * S::FT +
-             (size_t)w * S::FCW * D;
+    auto load_f = [&](int l) {
+      const float* t = tile(l) + (size_t)NB * (S::QT + S::PT) + (size_t)vb * S::FT + (size_t)w * S::FCW * D;
+      load_chunks(rf, t, true);
     };
-    auto tile_m = [&](int l) {
-      return p.tiles + (size_t)l * S::LAYER + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)blk * S::MT +
-             (size_t)w * 4 * D;
+    auto load_m = [&](int l) {
+      const float* t = tile(l) + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)vb * S::MT +
+                       (size_t)w * G * S::MJ * 256;
+      load_chunks(rm, t, true);
     };
     // cached K/V rows of this wave's keys in layer l, through buffer resources
     // bounded by the head's ctx rows (rows at or past the new one are masked
@@ -562,13 +639,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
 #define TD(i) \
   if (l == 1) trace_mark_d(p.trace, 160 + (i))
     load_ln(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B);
-    load_q(tile_q(0), true);
-    load_chunks(rp, tile_p(0), true);
+    load_q(0, true);
+    load_p(0, true);
     load_kv(0, wave_keys);
 
     for (int l = 0; l < p.L; l++) {
       const unsigned tb = tagbase + PH * l;
-      const unsigned tA = tb, tC = tb + 3, tD = tb + 4, tE = tb + 5;
+      const unsigned tA = tb, tC = tb + 3, tD = tb + 5, tE = tb + 6;
       const bool more = l + 1 < p.L;
       const float* vl = p.vecs + (size_t)l * S::VL;
       const float* vn = p.vecs + (size_t)(l + 1) * S::VL;  // next layer's (or ln_f after the last)
@@ -578,7 +655,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       {
         float4 xn[KC];
         ln_lane<KC, D>(xres, lnw, lnb, xn);
-        TD(1);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::QCW; t++) {
@@ -600,16 +676,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
             (part == 2 ? p.vc : p.kc)[(((size_t)l * H + h) * ctx + pos) * 64 + e] = s;
           }
         }
-        TD(2);
+        TD(1);
         // prefetches go after the output: a wave with many loads in flight can stall at issue
         load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
-        load_chunks(rf, tile_f(l), true);
-        TD(3);
+        load_f(l);
       }
       // ---- B: attention of head ah over key block kb ----
       if (attn_blk) {
         SYNC_OK();
-        TD(12);
+        TD(2);
         if (wave_keys) {
           // lane l: dims 4*(l % 16) .. +3 of keys key0 + 4i + l / 16, i < KPW / 4
           const int g = lane >> 4, d4 = 4 * (lane & 15);
@@ -655,7 +730,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
             wl[w] = lw;
           }
           if (g == 0) *reinterpret_cast<float4*>(&wo[w][d4]) = o4;
-          TD(13);
         } else {
           if (lane == 0) {
             wm[w] = -INFINITY;
@@ -663,31 +737,35 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           }
           wo[w][lane] = 0.f;
         }
+        TD(3);
         __syncthreads();
       }
-      load_chunks(rm, tile_m(l), true);
-      // ---- C: attn.proj + residual -> x2 ----
+      load_m(l);
+      // ---- C: this XCD's part of attn.proj over its heads' o ----
       SYNC_OK();
       TD(4);
       {
-        float acc = 0.f;
+        const int d4 = 4 * (lane & 15), r = lane >> 4;
 #pragma unroll
-        for (int c = 0; c < KC; c++) acc += dot4(rp[c], *reinterpret_cast<const float4*>(os + c * 256 + lane * 4));
-        const float v = wave_sum_dpp(acc);
-        if (lane == 0) {
-          const int col = blk * S::PCOL + w;
-          put_pair(p.uc + U::X2 + col, (v + bias_s[l & 1][S::B_P + w]) + xres[col], tC);
+        for (int g = 0; g < G; g++) {
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < S::PJ; j++) {
+            const float d = dot4(rp[j * G + g], *reinterpret_cast<const float4*>(os + j * 64 + d4));
+            acc += j < nh ? d : 0.f;  // o of a missing head is stale LDS
+          }
+          acc = row16_sum(acc);
+          if ((lane & 15) == 0) put_pair(p.uc + U::PX2 + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tC);
         }
         TD(5);
-        load_q(tile_q(more ? l + 1 : l), more);
+        load_q(more ? l + 1 : l, more);
       }
-      // ---- D: LN2 + mlp.fc + GELU -> h ----
+      // ---- D: LN2 + mlp.fc + GELU -> this XCD's h slice ----
       SYNC_OK();
       TD(6);
       {
         float4 xn[KC];
         ln_lane<KC, D>(x2s, lnw, lnb, xn);
-        TD(7);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::FCW; t++) {
@@ -699,27 +777,29 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
         }
         if (lane < S::FCW) {
           const int c = w * S::FCW + lane;
-          put_pair(p.uc + U::HH + blk * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
+          put_pair(xl + XL::HH + slot * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
         }
-        TD(8);
+        TD(7);
         load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
       }
-      // ---- E: mlp.proj + residual -> x ----
+      // ---- E: this XCD's part of mlp.proj over its h slice ----
       SYNC_OK();
-      TD(9);
+      TD(8);
       {
-        float acc = 0.f;
+        const int d4 = 4 * (lane & 15), r = lane >> 4;
 #pragma unroll
-        for (int c = 0; c < KC4; c++) acc += dot4(rm[c], *reinterpret_cast<const float4*>(hs + c * 256 + lane * 4));
-        const float v = wave_sum_dpp(acc);
-        if (lane == 0) {
-          const int col = blk * S::PCOL + w;
-          put_pair(p.uc + U::X + col, (v + bias_s[l & 1][S::B_M + w]) + x2s[col], tE);
+        for (int g = 0; g < G; g++) {
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < S::MJ; j++)
+            acc += dot4(rm[g * S::MJ + j], *reinterpret_cast<const float4*>(hs + j * 64 + d4));
+          acc = row16_sum(acc);
+          if ((lane & 15) == 0) put_pair(p.uc + U::PX + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tE);
         }
-        TD(10);
-        load_chunks(rp, tile_p(more ? l + 1 : l), more);
+        TD(9);
+        load_p(more ? l + 1 : l, more);
         load_kv(more ? l + 1 : l, more && wave_keys);
-        TD(11);
+        TD(10);
       }
     }
 #undef TD
@@ -803,13 +883,24 @@ __global__ void k_relayout(const float* __restrict__ W, int K, int N, const int*
   tile[i] = col >= 0 ? W[(size_t)k * N + col] : 0.f;
 }
 
-// out[b*32 + j] = src[map[b*ncol + j]] for j < ncol (one bias slice of the table)
+// chunks of 4 columns x 64 rows: tile[ch*256 + 4l + q] = W[k0 + 4*(l%16) + q][c0 + l/16]
+// for desc[ch] = (k0, c0); zeros where k0 < 0.  W row-major [K][N].
+__global__ void k_relayout_chunks(const float* __restrict__ W, int N, const int2* __restrict__ desc, int nchunks,
+                                  float* __restrict__ tile) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (size_t)nchunks * 256) return;
+  const int2 d = desc[i / 256];
+  const int e = (int)(i % 256), l = e / 4, q = e % 4;
+  tile[i] = d.x >= 0 ? W[(size_t)(d.x + 4 * (l % 16) + q) * N + d.y + l / 16] : 0.f;
+}
+
+// out[b*bt + off + j] = src[map[b*ncol + j]] for j < ncol (one bias slice of the table)
 __global__ void k_gather_bias(const float* __restrict__ src, const int* __restrict__ map, int ncol, int off,
-                              float* __restrict__ out) {
+                              int bt, float* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= NB * ncol) return;
   const int b = i / ncol, j = i % ncol, col = map[i];
-  out[b * 32 + off + j] = col >= 0 ? src[col] : 0.f;
+  out[b * bt + off + j] = col >= 0 ? src[col] : 0.f;
 }
 
 __global__ void k_copy(const float* __restrict__ src, float* __restrict__ dst, int n) {
@@ -850,25 +941,48 @@ using S768 = Shape<kD, kH>;
 size_t uc_pairs_bytes(int D) { return (size_t)Xu<kD>::NPAIR * sizeof(uint2) * (D / kD); }
 size_t uc_total_bytes(int D) { return (uc_pairs_bytes(D) + 255) / 256 * 256 + (size_t)NB * sizeof(uint4); }
 
-// column maps (host): qkv by XCD head ownership, stored under the virtual block
-// id b = slot * 8 + XCD; the others contiguous per block
-void make_maps(int D, int H, std::vector<int>& q, std::vector<int>& pr, std::vector<int>& fc) {
+// Host maps, all per virtual block vb = slot * 8 + XCD:
+//   q  qkv columns by XCD head ownership          f  mlp.fc columns: the XCD's h slice
+//   pc attn.proj chunks (head piece, wave, group)  mc mlp.proj chunks (wave, group, row piece)
+//   rs the slot's reduce columns (biases of attn.proj / mlp.proj)
+struct Maps {
+  std::vector<int> q, f, rs;
+  std::vector<int2> pc, mc;
+};
+
+Maps make_maps(int D, int H) {
   using S = S768;
-  q.assign((size_t)NB * S::QCMAX, -1);
-  for (int b = 0; b < NB; b++) {
-    const int x = b % NX, s = b / NX;
+  Maps m;
+  m.q.assign((size_t)NB * S::QCMAX, -1);
+  m.f.resize((size_t)NB * S::FCOL);
+  m.rs.resize((size_t)NB * S::RSC);
+  m.pc.resize((size_t)NB * S::PJ * NDW * S::G);
+  m.mc.resize((size_t)NB * NDW * S::G * S::MJ);
+  for (int vb = 0; vb < NB; vb++) {
+    const int x = vb % NX, s = vb / NX;
     const int nh = (H - x + NX - 1) / NX;
     const int qc = 3 * 64 * nh / SLOTS;
     for (int c = 0; c < qc; c++) {
       const int i = s * qc + c, j = i / 192, r = i % 192, part = r / 64, e = r % 64;
-      const int h = x + NX * j;
-      q[(size_t)b * S::QCMAX + c] = part * D + h * 64 + e;
+      m.q[(size_t)vb * S::QCMAX + c] = part * D + (x + NX * j) * 64 + e;
     }
+    for (int c = 0; c < S::FCOL; c++) m.f[(size_t)vb * S::FCOL + c] = x * S::HX + s * S::FCOL + c;
+    for (int c = 0; c < S::RSC; c++) m.rs[(size_t)vb * S::RSC + c] = s * S::RSC + c;
+    for (int j = 0; j < S::PJ; j++)
+      for (int w = 0; w < NDW; w++)
+        for (int g = 0; g < S::G; g++) {
+          const int c0 = s * S::RSC + w * 4 * S::G + 4 * g;
+          m.pc[(size_t)vb * S::PJ * NDW * S::G + (j * NDW + w) * S::G + g] =
+              j < nh ? make_int2((x + NX * j) * 64, c0) : make_int2(-1, -1);
+        }
+    for (int w = 0; w < NDW; w++)
+      for (int g = 0; g < S::G; g++)
+        for (int pc = 0; pc < S::MJ; pc++) {
+          const int c0 = s * S::RSC + w * 4 * S::G + 4 * g;
+          m.mc[(size_t)vb * NDW * S::G * S::MJ + (w * S::G + g) * S::MJ + pc] = make_int2(x * S::HX + 64 * pc, c0);
+        }
   }
-  pr.resize((size_t)NB * S::PCOL);
-  for (int i = 0; i < NB * S::PCOL; i++) pr[i] = i;
-  fc.resize((size_t)NB * S::FCOL);
-  for (int i = 0; i < NB * S::FCOL; i++) fc[i] = i;
+  return m;
 }
 
 }  // namespace
@@ -930,14 +1044,16 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
 int FastDecode::build(hipStream_t st, const float* const* params) {
   if (!enabled) return FH_OK;
   using S = S768;
-  std::vector<int> qm, pm, fm;
-  make_maps(D, H, qm, pm, fm);
-  int* dmap = nullptr;
-  const size_t nmap = qm.size() + pm.size() + fm.size();
-  if (hipMalloc(&dmap, nmap * sizeof(int)) != hipSuccess) return FH_ERR_OOM;
-  int* dq = dmap;
-  int* dp = dq + qm.size();
-  int* df = dp + pm.size();
+  const Maps m = make_maps(D, H);
+  char* dmap = nullptr;
+  const size_t nq = m.q.size() * 4, nf = m.f.size() * 4, nr = m.rs.size() * 4, np = m.pc.size() * 8,
+               nmc = m.mc.size() * 8;
+  if (hipMalloc(&dmap, nq + nf + nr + np + nmc) != hipSuccess) return FH_ERR_OOM;
+  int* dq = reinterpret_cast<int*>(dmap);
+  int* df = reinterpret_cast<int*>(dmap + nq);
+  int* dr = reinterpret_cast<int*>(dmap + nq + nf);
+  int2* dp = reinterpret_cast<int2*>(dmap + nq + nf + nr);
+  int2* dm = reinterpret_cast<int2*>(dmap + nq + nf + nr + np);
   int rc = FH_OK;
   auto copy = [&](const float* src, float* dst, int n) {
     hipLaunchKernelGGL(k_copy, dim3((n + 255) / 256), dim3(256), 0, st, src, dst, n);
@@ -948,13 +1064,22 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
     hipLaunchKernelGGL(k_relayout, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, W, K, N, map, ncol, out);
     return hipGetLastError() == hipSuccess;
   };
-  auto bias = [&](const float* src, const int* map, int ncol, int off, float* out) {
-    hipLaunchKernelGGL(k_gather_bias, dim3((NB * ncol + 255) / 256), dim3(256), 0, st, src, map, ncol, off, out);
+  auto chunks = [&](const float* W, int N, const int2* desc, int nch, float* out) {
+    const size_t tot = (size_t)nch * 256;
+    hipLaunchKernelGGL(k_relayout_chunks, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, W, N, desc, nch,
+                       out);
     return hipGetLastError() == hipSuccess;
   };
-  if (hipMemcpy(dq, qm.data(), qm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(dp, pm.data(), pm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(df, fm.data(), fm.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+  auto bias = [&](const float* src, const int* map, int ncol, int off, float* out) {
+    hipLaunchKernelGGL(k_gather_bias, dim3((NB * ncol + 255) / 256), dim3(256), 0, st, src, map, ncol, off, S::BT,
+                       out);
+    return hipGetLastError() == hipSuccess;
+  };
+  if (hipMemcpy(dq, m.q.data(), nq, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(df, m.f.data(), nf, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dr, m.rs.data(), nr, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dp, m.pc.data(), np, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(dm, m.mc.data(), nmc, hipMemcpyHostToDevice) != hipSuccess)
     rc = FH_ERR_HIP;
   for (int l = 0; l < L && rc == FH_OK; l++) {
     float* tl = tiles + (size_t)l * S::LAYER;
@@ -962,11 +1087,11 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
     float* bt = btab + (size_t)l * NB * S::BT;
     // registry slots: 0 ln1.w 1 ln1.b 2 qkv.w 3 qkv.b 4 proj.w 5 proj.b 6 ln2.w 7 ln2.b 8 fc.w 9 fc.b 10 mproj.w 11 mproj.b
     const bool good = relayout(PL[2], D, 3 * D, dq, S::QCMAX, tl) &&
-                      relayout(PL[4], D, D, dp, S::PCOL, tl + (size_t)NB * S::QT) &&
+                      chunks(PL[4], D, dp, (int)m.pc.size(), tl + (size_t)NB * S::QT) &&
                       relayout(PL[8], D, 4 * D, df, S::FCOL, tl + (size_t)NB * (S::QT + S::PT)) &&
-                      relayout(PL[10], 4 * D, D, dp, S::PCOL, tl + (size_t)NB * (S::QT + S::PT + S::FT)) &&
-                      bias(PL[3], dq, S::QCMAX, S::B_Q, bt) && bias(PL[5], dp, S::PCOL, S::B_P, bt) &&
-                      bias(PL[9], df, S::FCOL, S::B_F, bt) && bias(PL[11], dp, S::PCOL, S::B_M, bt);
+                      chunks(PL[10], D, dm, (int)m.mc.size(), tl + (size_t)NB * (S::QT + S::PT + S::FT)) &&
+                      bias(PL[3], dq, S::QCMAX, S::B_Q, bt) && bias(PL[9], df, S::FCOL, S::B_F, bt) &&
+                      bias(PL[5], dr, S::RSC, S::B_P, bt) && bias(PL[11], dr, S::RSC, S::B_M, bt);
     float* vl = vecs + (size_t)l * S::VL;
     if (!good || !copy(PL[0], vl + S::V_LN1W, D) || !copy(PL[1], vl + S::V_LN1B, D) ||
         !copy(PL[6], vl + S::V_LN2W, D) || !copy(PL[7], vl + S::V_LN2B, D))
