@@ -189,12 +189,14 @@ struct KParams {
   unsigned long long* trace;  // optional: block 0 timestamps
 };
 
+// Optional timestamps (FORGE_HIP_TRACE=1): TRACE_PER entries per block, written
+// by the control wave (marks 0..15, 30, 31) and data wave 0 (marks 16..29).
+constexpr int TRACE_PER = 32;
 __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
-  if (t && blockIdx.x == 0 && threadIdx.x == (NT - 64) && i < 256) t[i] = wall_clock64();
+  if (t && threadIdx.x == (NT - 64)) t[blockIdx.x * TRACE_PER + i] = wall_clock64();
 }
-// same, from data wave 0
 __device__ __forceinline__ void trace_mark_d(unsigned long long* t, int i) {
-  if (t && blockIdx.x == 0 && threadIdx.x == 0 && i < 256) t[i] = wall_clock64();
+  if (t && threadIdx.x == 0) t[blockIdx.x * TRACE_PER + 16 + i] = wall_clock64();
 }
 
 // Control wave: waits until pairs[pair0, pair0 + n) all carry `tag` (n <= N),
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   const int vb = slot * NX + xcd;
   if (tid == 0) fail_s = 0;
   const unsigned tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
-  trace_mark(p.trace, 0);
+  trace_mark(p.trace, 30);
 
   const int n = *p.src.step;
   const int pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token (>= 1)
@@ -402,7 +404,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     // ================= control wave: collects every hand-off =================
     const NcBuf ncu(p.uc, p.uc_bytes), ncl(p.xl, p.xl_bytes);
 #define TM(i) \
-  if (l == 1) trace_mark(p.trace, 128 + (i))
+  if (l == 1) trace_mark(p.trace, (i))
     for (int l = 0; l < p.L; l++) {
       const unsigned tb = tagbase + PH * l;
       const unsigned tA = tb, tP = tb + 1, tB = tb + 2, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6,
@@ -489,6 +491,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       TM(3);
       // ---- x2 = x + attn.proj(o) + b: this slot's columns from the 8 XCD partials ----
       if (!gather_slices<D, RSC>(ncu, U::PX2, slot, tC, rsv, p.err, err_code(W_PX2, l))) fail_s = 1;
+      TM(7);
       wave_lds_sync();
       if (lane < RSC) {
         float sum = 0.f;
@@ -506,6 +509,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       TM(5);
       // ---- E: x = x2 + mlp.proj(h) + b: this slot's columns from the 8 XCD partials ----
       if (!gather_slices<D, RSC>(ncu, U::PX, slot, tE, rsv, p.err, err_code(W_PX, l))) fail_s = 1;
+      TM(8);
       wave_lds_sync();
       if (lane < RSC) {
         float sum = 0.f;
@@ -570,11 +574,11 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     // ================= data waves: weights in registers =================
     const int key0 = kb * KPB + w * KPW;  // this data wave's first key
     const bool wave_keys = attn_blk && key0 < nk;
-    // Register tiles, each requested two phases before its use; every load is
-    // unconditional (an empty buffer resource when there is nothing to fetch),
-    // so no register stays live across the whole layer loop:
-    //   after A: rf(l), LN2(l)   after B: rm(l)   after C: rq(l+1)
-    //   after D: LN1(l+1)        after E: rp(l+1), K/V(l+1)
+    // Register tiles, each requested at least two phases before its use;
+    // every register is loaded on every path (an empty buffer resource when
+    // there is nothing to fetch), so none stays live across the whole loop:
+    //   attention blocks   A: rf(l), LN2(l)  B: rm(l)  C: rq(l+1)  D: LN1(l+1)  E: rp(l+1), K/V(l+1)
+    //   the others         A: rf(l), LN2(l), rm(l), rq(l+1)  C: rp(l+1)  D: LN1(l+1)
     float4 rq[S::QCW * KC], rp[S::PJ * G], rf[S::FCW * KC], rm[G * S::MJ];
     // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
     // lane l the dims 4*(l % 16) .. +3 of row key0 + 4i + l / 16 (one 1 KB load each)
@@ -637,7 +641,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       for (int i = 0; i < KPW / 4; i++) vr[i] = ld4(rv, off + 1024 * i);
     };
 #define TD(i) \
-  if (l == 1) trace_mark_d(p.trace, 160 + (i))
+  if (l == 1) trace_mark_d(p.trace, (i))
     load_ln(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B);
     load_q(0, true);
     load_p(0, true);
@@ -652,9 +656,16 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       // ---- A: LN1 + QKV ----
       SYNC_OK();
       TD(0);
+      // Bulk prefetches share this CU's memory queue with the control wave's
+      // polls and block the issuing wave while the queue drains.  Blocks
+      // without attention work issue almost all of theirs right after A,
+      // while the attention blocks keep the chip's critical path; attention
+      // blocks spread theirs over the phases.
+      if (attn_blk) load_f(l);
       {
         float4 xn[KC];
         ln_lane<KC, D>(xres, lnw, lnb, xn);
+        if (attn_blk) load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::QCW; t++) {
@@ -677,14 +688,18 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           }
         }
         TD(1);
-        // prefetches go after the output: a wave with many loads in flight can stall at issue
-        load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
-        load_f(l);
+        if (!attn_blk) {
+          load_f(l);
+          load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
+          load_m(l);
+          load_q(more ? l + 1 : l, more);
+        }
       }
       // ---- B: attention of head ah over key block kb ----
       if (attn_blk) {
         SYNC_OK();
         TD(2);
+        load_m(l);
         if (wave_keys) {
           // lane l: dims 4*(l % 16) .. +3 of keys key0 + 4i + l / 16, i < KPW / 4
           const int g = lane >> 4, d4 = 4 * (lane & 15);
@@ -693,6 +708,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           const float4 vnew = *reinterpret_cast<const float4*>(qkvs + 128 + d4);
           float sc[KPW / 4];
           float mloc = -INFINITY;
+          if (l == 1 && p.trace) {  // trace: wait for the K/V rows before timing the scores
+            float z = kr[0].x + vr[KPW / 4 - 1].w;
+            asm volatile("" : "+v"(z));
+            if (z == 1234.5f) mloc = 0.f;
+            TD(11);
+          }
 #pragma unroll
           for (int i = 0; i < KPW / 4; i++) {
             const int j = key0 + 4 * i + g;
@@ -702,6 +723,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
             mloc = fmaxf(mloc, sc[i]);
           }
           const float mw = wave_max_dpp(mloc);
+          TD(12);
           float lloc = 0.f;
           float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
@@ -740,10 +762,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
         TD(3);
         __syncthreads();
       }
-      load_m(l);
       // ---- C: this XCD's part of attn.proj over its heads' o ----
       SYNC_OK();
       TD(4);
+      if (attn_blk) load_q(more ? l + 1 : l, more);
       {
         const int d4 = 4 * (lane & 15), r = lane >> 4;
 #pragma unroll
@@ -758,7 +780,10 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           if ((lane & 15) == 0) put_pair(p.uc + U::PX2 + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tC);
         }
         TD(5);
-        load_q(more ? l + 1 : l, more);
+        if (!attn_blk) {
+          load_p(more ? l + 1 : l, more);
+          load_kv(l, false);  // nothing to fetch; keeps kr / vr written on every path
+        }
       }
       // ---- D: LN2 + mlp.fc + GELU -> this XCD's h slice ----
       SYNC_OK();
@@ -766,6 +791,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
       {
         float4 xn[KC];
         ln_lane<KC, D>(x2s, lnw, lnb, xn);
+        load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::FCW; t++) {
@@ -780,11 +806,14 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           put_pair(xl + XL::HH + slot * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
         }
         TD(7);
-        load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
       }
       // ---- E: this XCD's part of mlp.proj over its h slice ----
       SYNC_OK();
       TD(8);
+      if (attn_blk) {
+        load_p(more ? l + 1 : l, more);
+        load_kv(more ? l + 1 : l, more && wave_keys);
+      }
       {
         const int d4 = 4 * (lane & 15), r = lane >> 4;
 #pragma unroll
@@ -797,9 +826,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           if ((lane & 15) == 0) put_pair(p.uc + U::PX + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tE);
         }
         TD(9);
-        load_p(more ? l + 1 : l, more);
-        load_kv(more ? l + 1 : l, more && wave_keys);
-        TD(10);
       }
     }
 #undef TD
@@ -865,7 +891,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     }
   }
 #undef SYNC_OK
-  trace_mark(p.trace, 127);
+  trace_mark(p.trace, 31);
 }
 
 __global__ void k_xcc_probe(unsigned* out) {
@@ -1034,8 +1060,8 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   if (reset_state() != FH_OK) return FH_ERR_HIP;
   const char* tr = getenv("FORGE_HIP_TRACE");
   if (tr && tr[0] == '1') {
-    if (hipMalloc(&trace, 256 * sizeof(unsigned long long)) != hipSuccess) return FH_ERR_OOM;
-    if (hipMemset(trace, 0, 256 * sizeof(unsigned long long)) != hipSuccess) return FH_ERR_HIP;
+    if (hipMalloc(&trace, (size_t)NB * TRACE_PER * sizeof(unsigned long long)) != hipSuccess) return FH_ERR_OOM;
+    if (hipMemset(trace, 0, (size_t)NB * TRACE_PER * sizeof(unsigned long long)) != hipSuccess) return FH_ERR_HIP;
   }
   enabled = true;
   return FH_OK;

@@ -26,7 +26,7 @@ struct FastDecode {
   void* ctl = nullptr;  // launch counter (word 0), error word (16)
   unsigned counter = 1;                 // launch counter value set at the last reset
   unsigned long long launched = 0;      // launches since that reset
-  unsigned long long* trace = nullptr;  // timestamps of the last step (FORGE_HIP_TRACE=1)
+  unsigned long long* trace = nullptr;  // per-block timestamps of the last step (FORGE_HIP_TRACE=1), 256 x 32
   size_t tile_floats = 0;
 
   int init(const fh_model_desc& d, int compute_units);

@@ -915,13 +915,13 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   return FH_OK;
 }
 
-// Debug helper (not part of the public header): block-0 timestamps of the last
-// fused decode step when the session was created with FORGE_HIP_TRACE=1.
+// Debug helper (not part of the public header): per-block timestamps (256 x 32)
+// of the last fused decode step when the session was created with FORGE_HIP_TRACE=1.
 int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n) {
   if (!s || !out || n < 0) return set_err(FH_ERR_INVALID, "bad argument");
   if (!s->fast.trace) return set_err(FH_ERR_STATE, "tracing is off (set FORGE_HIP_TRACE=1 before creating the session)");
   HIP_TRY(hipStreamSynchronize(s->ctx->stream));
-  HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256), hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256 * 32), hipMemcpyDeviceToHost));
   return FH_OK;
 }
 
