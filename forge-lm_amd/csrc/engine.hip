@@ -168,6 +168,9 @@ struct fh_session {
   std::vector<size_t> off;  // byte offsets in wbuf
   char* wbuf = nullptr;
   size_t wbytes = 0;
+  // per layer, the four matrices transposed to [N][K] (session dtype) for the MFMA GEMM
+  char* wtbuf = nullptr;
+  std::vector<size_t> wtoff;  // byte offset in wtbuf per registry slot (matrices of blocks only)
   bool loaded = false;
   int esize = 4;  // bytes per matrix element
   // KV cache
@@ -205,6 +208,10 @@ struct fh_session {
   template <typename T>
   const T* w(size_t i) const {
     return reinterpret_cast<const T*>(wbuf + off[i]);
+  }
+  template <typename T>
+  const T* wt(size_t i) const {
+    return reinterpret_cast<const T*>(wtbuf + wtoff[i]);
   }
   const float* v(size_t i) const { return reinterpret_cast<const float*>(wbuf + off[i]); }
   size_t idx_tok() const { return 0; }
@@ -260,18 +267,22 @@ int check_launch(hipError_t e, const char* what) {
 
 #define LAUNCH(expr) FH_TRY(check_launch((expr), #expr))
 
-// y = epi(x @ W + b) (+ res) for M rows; split-K GEMV when M <= 4.
+// y = epi(x @ W + b) (+ res) for registry matrix `slot`: split-K GEMV for up to
+// 4 rows, the MFMA GEMM on the transposed copy above that.
 template <typename WT>
-int linear(fh_session* s, const float* x, int M, int K, const WT* W, int N, const float* b, int epi, const float* res,
+int linear(fh_session* s, const float* x, int M, int K, size_t slot, int N, const float* b, int epi, const float* res,
            float* y) {
   hipStream_t st = s->ctx->stream;
   if (M <= 4) {
     int S = 0;
     int splits = std::max(1, std::min(64, K / 16));
-    LAUNCH(launch_gemv_splitk<WT>(st, x, M, K, W, N, s->part, splits, &S));
+    LAUNCH(launch_gemv_splitk<WT>(st, x, M, K, s->w<WT>(slot), N, s->part, splits, &S));
     LAUNCH(launch_splitk_epilogue(st, s->part, S, M, N, b, epi, res, y));
-  } else {
-    LAUNCH(launch_gemm<WT>(st, x, M, K, W, N, b, epi, res, y));
+  } else if (K % 32 == 0) {
+    LAUNCH(launch_gemm_mfma<WT>(st, x, M, K, s->wt<WT>(slot), N, b, epi, res, y, s->part, s->part_floats,
+                                s->ctx->props.multiProcessorCount));
+  } else {  // tiny models (K not a multiple of 32): the plain tiled GEMM
+    LAUNCH(launch_gemm<WT>(st, x, M, K, s->w<WT>(slot), N, b, epi, res, y));
   }
   return FH_OK;
 }
@@ -284,15 +295,15 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
     LAUNCH(launch_layernorm(st, s->x, M, M, 0, 0, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), s->xn, D, 1e-5f));
-    FH_TRY(linear<WT>(s, s->xn, M, D, s->w<WT>(s->idx_blk(l, 2)), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
+    FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 2), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, T, D, H, C, kc, vc));
     LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
-    FH_TRY(linear<WT>(s, s->o, M, D, s->w<WT>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
+    FH_TRY(linear<WT>(s, s->o, M, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
     LAUNCH(launch_layernorm(st, s->x2, M, M, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
-    FH_TRY(linear<WT>(s, s->xn, M, D, s->w<WT>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+    FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
                       s->h));
-    FH_TRY(linear<WT>(s, s->h, M, 4 * D, s->w<WT>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
+    FH_TRY(linear<WT>(s, s->h, M, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
                       s->x));
   }
   return FH_OK;
@@ -306,15 +317,15 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
     LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), s->xn, D, 1e-5f));
-    FH_TRY(linear<WT>(s, s->xn, B, D, s->w<WT>(s->idx_blk(l, 2)), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
+    FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 2), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, 1, D, H, C, kc, vc));
     LAUNCH(launch_attn_decode<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, 64, s->o));
-    FH_TRY(linear<WT>(s, s->o, B, D, s->w<WT>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
+    FH_TRY(linear<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
     LAUNCH(launch_layernorm(st, s->x2, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
-    FH_TRY(linear<WT>(s, s->xn, B, D, s->w<WT>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+    FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
                       s->h));
-    FH_TRY(linear<WT>(s, s->h, B, 4 * D, s->w<WT>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
+    FH_TRY(linear<WT>(s, s->h, B, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
                       s->x));
   }
   return FH_OK;
@@ -483,6 +494,22 @@ int upload_weights(fh_session* s, const float* const* tensors) {
     }
     HIP_TRY(hipMemcpy(s->wbuf + s->off[i], p, bytes, hipMemcpyHostToDevice));
   }
+  // [K][N] -> [N][K] copies of every block matrix for the MFMA GEMM
+  {
+    const int64_t D = s->d.d_model;
+    for (int l = 0; l < s->d.n_layers; l++)
+      for (int k : {2, 4, 8, 10}) {
+        const size_t i = s->idx_blk(l, k);
+        const int K = (int)(k == 10 ? 4 * D : D);
+        const int N = (int)(s->reg[i].numel / K);
+        hipError_t e = bf ? launch_transpose<bf16_t>(s->ctx->stream, s->w<bf16_t>(i), K, N,
+                                                     reinterpret_cast<bf16_t*>(s->wtbuf + s->wtoff[i]))
+                          : launch_transpose<float>(s->ctx->stream, s->w<float>(i), K, N,
+                                                    reinterpret_cast<float*>(s->wtbuf + s->wtoff[i]));
+        HIP_TRY(e);
+      }
+    HIP_TRY(hipStreamSynchronize(s->ctx->stream));
+  }
   s->loaded = true;
   drop_graph(s->g_decode);
   drop_graph(s->g_reprefill);
@@ -621,6 +648,46 @@ int fh_buffer_copy(fh_context* c, void* dst_dev, const void* src_dev, size_t byt
   return FH_OK;
 }
 
+int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_dev, int M, int K, int N, int dtype,
+                 int accumulate) {
+  if (!c || !a_dev || !b_dev || !y_dev) return set_err(FH_ERR_INVALID, "null argument");
+  if (M <= 0 || K <= 0 || N <= 0) return set_err(FH_ERR_INVALID, "M, K and N must be positive");
+  if (dtype != FH_DTYPE_F32 && dtype != FH_DTYPE_BF16) return set_err(FH_ERR_INVALID, "unknown dtype %d", dtype);
+  HIP_TRY(hipSetDevice(c->device));
+  hipStream_t st = c->stream;
+  const float* a = static_cast<const float*>(a_dev);
+  float* y = static_cast<float*>(y_dev);
+  const float* res = accumulate ? y : nullptr;  // each output element is read, then written, by one lane
+  const bool bf = dtype == FH_DTYPE_BF16;
+  hipError_t e = hipSuccess;
+  if (K % 32 == 0) {
+    // the GEMM takes the weights transposed, plus room for split-K partials
+    const size_t esz = bf ? 2 : 4, part_floats = (size_t)8 * M * N;
+    char* tmp = nullptr;
+    HIP_TRY(hipMalloc(&tmp, (size_t)N * K * esz + part_floats * 4));
+    float* part = reinterpret_cast<float*>(tmp + (size_t)N * K * esz);
+    if (bf) {
+      e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, reinterpret_cast<bf16_t*>(tmp));
+      if (e == hipSuccess)
+        e = launch_gemm_mfma<bf16_t>(st, a, M, K, reinterpret_cast<const bf16_t*>(tmp), N, nullptr, EPI_NONE, res, y,
+                                     part, part_floats, c->props.multiProcessorCount);
+    } else {
+      e = launch_transpose<float>(st, static_cast<const float*>(b_dev), K, N, reinterpret_cast<float*>(tmp));
+      if (e == hipSuccess)
+        e = launch_gemm_mfma<float>(st, a, M, K, reinterpret_cast<const float*>(tmp), N, nullptr, EPI_NONE, res, y,
+                                    part, part_floats, c->props.multiProcessorCount);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(tmp);
+  } else {
+    e = bf ? launch_gemm<bf16_t>(st, a, M, K, static_cast<const bf16_t*>(b_dev), N, nullptr, EPI_NONE, res, y)
+           : launch_gemm<float>(st, a, M, K, static_cast<const float*>(b_dev), N, nullptr, EPI_NONE, res, y);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+  }
+  HIP_TRY(e);
+  return FH_OK;
+}
+
 int64_t fh_param_count(const fh_model_desc* d) {
   if (validate_desc(d) != FH_OK) return -1;
   int64_t n = 0;
@@ -656,6 +723,15 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
     o += ((size_t)sl.numel * (sl.matrix ? s->esize : 4) + 255) / 256 * 256;
   }
   s->wbytes = o;
+  // transposed copies of the blocks' matrices (tok_emb / pos_emb are not needed)
+  size_t ot = 0;
+  s->wtoff.assign(s->reg.size(), 0);
+  for (size_t i = 2; i < s->reg.size(); i++)
+    if (s->reg[i].matrix) {
+      s->wtoff[i] = ot;
+      ot += ((size_t)s->reg[i].numel * s->esize + 255) / 256 * 256;
+    }
+  const size_t wtbytes = ot;
   fh_session* sp = s.get();
   auto fail = [&](int rc) {
     fh_session_destroy(s.release());
@@ -663,6 +739,7 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
   };
   int rc;
   if ((rc = dev_alloc(&sp->wbuf, sp->wbytes)) != FH_OK) return fail(rc);
+  if ((rc = dev_alloc(&sp->wtbuf, wtbytes)) != FH_OK) return fail(rc);
   const int B = desc->max_batch, D = desc->d_model, C = desc->context_length, V = desc->vocab_size;
   const int H = desc->n_heads, hd = D / H;
   sp->kv_layer = (size_t)B * H * C * hd;
@@ -675,7 +752,9 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
   sp->vc = vc;
   const size_t rows = (size_t)B * C;
   const int maxc = (C + 63) / 64;
-  sp->part_floats = (size_t)64 * 4 * 4 * D;
+  // split-K partials: the GEMV path (up to 64 splits of 4 rows) and the MFMA
+  // GEMM's small-M split (up to 8 splits of 64 rows of the widest layer)
+  sp->part_floats = std::max((size_t)64 * 4 * 4 * D, (size_t)8 * 64 * 4 * D);
   if ((rc = dev_alloc(&sp->x, rows * D)) || (rc = dev_alloc(&sp->x2, rows * D)) || (rc = dev_alloc(&sp->xn, rows * D)) ||
       (rc = dev_alloc(&sp->qkv, rows * 3 * D)) || (rc = dev_alloc(&sp->o, rows * D)) ||
       (rc = dev_alloc(&sp->h, rows * 4 * D)) || (rc = dev_alloc(&sp->part, sp->part_floats)) ||
@@ -707,6 +786,7 @@ int fh_session_destroy(fh_session* s) {
   for (auto& e : s->ev)
     if (e) (void)hipEventDestroy(e);
   dev_free(s->wbuf);
+  dev_free(s->wtbuf);
   char* kc = static_cast<char*>(s->kc);
   char* vc = static_cast<char*>(s->vc);
   dev_free(kc);

@@ -1,0 +1,244 @@
+// gemm_mfma.hip -- LDS-staged MFMA GEMM for gfx950: prefill and batched decode.
+//
+// Linear.Forward (src/LLM.Core/Layers/Layers.cs:29-37): y = x @ W + b for M
+// rows.  W comes pre-transposed as Wt[N][K] (k contiguous, built once per
+// session), so both MFMA operands are k-contiguous in global memory and in
+// LDS.  A block computes a BM x 128 tile of y; each of its 4 waves owns a
+// 32-column strip and BM/32 MFMA 32x32 accumulators.  K advances 32 per stage
+// through a double-buffered LDS pair: the next stage's global loads are in
+// registers while the current stage's MFMAs run.
+//
+//   bf16 sessions: v_mfma_f32_32x32x16_bf16; activations are rounded to bf16
+//                  on their way into LDS, accumulation is fp32.
+//   fp32 sessions: v_mfma_f32_32x32x2_f32 on exact fp32 operands; within a
+//                  32-wide k stage the LDS rows hold the even k first, then the
+//                  odd k, so each half-wave reads its k values as float4s.
+//
+// With S > 1 (blockIdx.z) each block covers K/S of the reduction and writes a
+// partial; launch_splitk_epilogue then sums the partials in order, adds the
+// bias (if any) and applies GELU / the residual.  With S == 1 the epilogue is
+// fused.
+#include "kernels.hpp"
+
+namespace fh {
+
+namespace {
+
+constexpr int BN = 128;  // columns per block (4 waves x 32)
+constexpr int BK = 32;   // k per stage
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// MFMA 32x32 accumulator layout: lane l holds column l % 32 and, in element r,
+// row (r / 4) * 8 + (l / 32) * 4 + r % 4.
+__device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
+
+template <typename WT>
+struct Tr;
+
+// ---- bf16: LDS rows of BK bf16 (+8 pad), fragments of 8 k per lane ----
+template <>
+struct Tr<bf16_t> {
+  static constexpr int LDK = BK + 8;  // bf16 per LDS row
+  typedef bf16_t elem;
+};
+
+// ---- fp32: LDS rows of BK floats (+4 pad), even k then odd k ----
+template <>
+struct Tr<float> {
+  static constexpr int LDK = BK + 4;
+  typedef float elem;
+};
+
+template <typename WT, int BM>
+__global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, int M, int K,
+                                                  const WT* __restrict__ Wt, int N, int kchunk,
+                                                  const float* __restrict__ bias, int epi,
+                                                  const float* __restrict__ res, float* __restrict__ Y,
+                                                  float* __restrict__ part) {
+  using E = typename Tr<WT>::elem;
+  constexpr int LDK = Tr<WT>::LDK;
+  constexpr int MT = BM / 32;  // MFMA tiles along M per wave
+  __shared__ __align__(16) E As[2][BM][LDK];
+  __shared__ __align__(16) E Bs[2][BN][LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int kb = blockIdx.z * kchunk, ke = min(K, kb + kchunk);
+  const int nst = (ke - kb) / BK;
+
+  // global -> register staging: A as float4 (BM*BK/4 per stage), W as 16 B
+  constexpr int AV = BM * BK / 4 / 256;  // float4 of A per thread per stage
+  constexpr int WB = BN * BK * (int)sizeof(WT) / 16 / 256;  // 16-byte pieces of W per thread per stage
+  static_assert(AV >= 1 && WB >= 1, "tile too small for 256 threads");
+  float4 ra[AV];
+  uint4 rw[WB];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < AV; i++) {
+      const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
+      ra[i] = (m0 + row < M) ? *reinterpret_cast<const float4*>(A + (size_t)(m0 + row) * K + k0 + 4 * kq)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    constexpr int PER_ROW = BK * (int)sizeof(WT) / 16;  // 16-byte pieces per W row and stage
+#pragma unroll
+    for (int i = 0; i < WB; i++) {
+      const int idx = tid + 256 * i, row = idx / PER_ROW, q = idx % PER_ROW;
+      rw[i] = (n0 + row < N) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(Wt + (size_t)(n0 + row) * K + k0) + 16 * q)
+                             : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto sstore = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < AV; i++) {
+      const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
+      if constexpr (sizeof(WT) == 2) {
+        const uint32_t lo = (uint32_t)f32_to_bf16(ra[i].x) | ((uint32_t)f32_to_bf16(ra[i].y) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(ra[i].z) | ((uint32_t)f32_to_bf16(ra[i].w) << 16);
+        *reinterpret_cast<uint2*>(&As[b][row][4 * kq]) = make_uint2(lo, hi);
+      } else {
+        // k = 4kq .. 4kq+3: even k to positions 2kq, 2kq+1; odd k to BK/2 + 2kq, +1
+        *reinterpret_cast<float2*>(&As[b][row][2 * kq]) = make_float2(ra[i].x, ra[i].z);
+        *reinterpret_cast<float2*>(&As[b][row][BK / 2 + 2 * kq]) = make_float2(ra[i].y, ra[i].w);
+      }
+    }
+    constexpr int PER_ROW = BK * (int)sizeof(WT) / 16;
+#pragma unroll
+    for (int i = 0; i < WB; i++) {
+      const int idx = tid + 256 * i, row = idx / PER_ROW, q = idx % PER_ROW;
+      if constexpr (sizeof(WT) == 2) {
+        *reinterpret_cast<uint4*>(&Bs[b][row][8 * q]) = rw[i];
+      } else {
+        const float4 v = make_float4(__uint_as_float(rw[i].x), __uint_as_float(rw[i].y), __uint_as_float(rw[i].z),
+                                     __uint_as_float(rw[i].w));
+        *reinterpret_cast<float2*>(&Bs[b][row][2 * q]) = make_float2(v.x, v.z);
+        *reinterpret_cast<float2*>(&Bs[b][row][BK / 2 + 2 * q]) = make_float2(v.y, v.w);
+      }
+    }
+  };
+
+  f32x16_t acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[t][r] = 0.f;
+
+  const int fr = lane & 31, fh = lane >> 5;  // fragment row / column and k half
+  if (nst > 0) {
+    gload(kb);
+    sstore(0);
+  }
+  __syncthreads();
+  for (int st = 0; st < nst; st++) {
+    const int b = st & 1;
+    if (st + 1 < nst) gload(kb + (st + 1) * BK);
+    if constexpr (sizeof(WT) == 2) {
+#pragma unroll
+      for (int kk = 0; kk < BK / 16; kk++) {
+        const bf16x8_t bf = *reinterpret_cast<const bf16x8_t*>(&Bs[b][w * 32 + fr][kk * 16 + 8 * fh]);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(&As[b][t * 32 + fr][kk * 16 + 8 * fh]);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[t], 0, 0, 0);
+        }
+      }
+    } else {
+      // k step s covers k = 2s (lanes 0..31) and 2s + 1 (lanes 32..63)
+#pragma unroll
+      for (int q = 0; q < BK / 8; q++) {
+        const float4 bq = *reinterpret_cast<const float4*>(&Bs[b][w * 32 + fr][fh * (BK / 2) + 4 * q]);
+        float4 aq[MT];
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+          aq[t] = *reinterpret_cast<const float4*>(&As[b][t * 32 + fr][fh * (BK / 2) + 4 * q]);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[t].x, bq.x, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[t].y, bq.y, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[t].z, bq.z, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[t].w, bq.w, acc[t], 0, 0, 0);
+        }
+      }
+    }
+    if (st + 1 < nst) sstore(b ^ 1);
+    __syncthreads();
+  }
+
+  const int col = n0 + w * 32 + fr;
+  if (col >= N) return;
+  const float bcol = (part || !bias) ? 0.f : bias[col];
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m0 + t * 32 + acc_row(lane, r);
+      if (row >= M) continue;
+      if (part) {
+        part[((size_t)blockIdx.z * M + row) * N + col] = acc[t][r];
+      } else {
+        float s = acc[t][r] + bcol;
+        if (epi == EPI_GELU) s = gelu_tanh(s);
+        if (res) s += res[(size_t)row * N + col];
+        Y[(size_t)row * N + col] = s;
+      }
+    }
+  }
+}
+
+// Wt[n][k] = W[k][n] (one-time weight transpose at session load), 32x32 LDS tiles
+template <typename WT>
+__global__ __launch_bounds__(256) void k_transpose(const WT* __restrict__ W, int K, int N, WT* __restrict__ Wt) {
+  __shared__ WT tile[32][33];
+  const int k0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (int i = ty; i < 32; i += 8)
+    if (k0 + i < K && n0 + tx < N) tile[i][tx] = W[(size_t)(k0 + i) * N + n0 + tx];
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8)
+    if (n0 + i < N && k0 + tx < K) Wt[(size_t)(n0 + i) * K + k0 + tx] = tile[tx][i];
+}
+
+}  // namespace
+
+template <typename WT>
+hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt) {
+  if (!W || !Wt || K <= 0 || N <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_transpose<WT>, dim3((N + 31) / 32, (K + 31) / 32), dim3(256), 0, st, W, K, N, Wt);
+  return hipGetLastError();
+}
+
+template <typename WT>
+hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, const float* bias,
+                            int epi, const float* res, float* y, float* part, size_t part_floats, int cus) {
+  if (!a || !Wt || !y || M <= 0 || N <= 0 || K <= 0 || K % BK != 0) return hipErrorInvalidValue;
+  const int gn = (N + BN - 1) / BN;
+  const int bm = M > 64 ? 128 : (M > 32 ? 64 : 32);
+  const int gm = (M + bm - 1) / bm;
+  // split K until the grid covers the CUs about twice (partials must fit)
+  int S = 1;
+  const int target = 2 * (cus > 0 ? cus : 256);
+  while (gn * gm * S * 2 <= target && (K / BK) % (S * 2) == 0 && (size_t)S * 2 * M * N <= part_floats && part)
+    S *= 2;
+  const int kchunk = K / S;
+  dim3 grid(gn, gm, S);
+  float* pp = S > 1 ? part : nullptr;
+  if (bm == 128)
+    hipLaunchKernelGGL((k_gemm_mfma<WT, 128>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+  else if (bm == 64)
+    hipLaunchKernelGGL((k_gemm_mfma<WT, 64>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+  else
+    hipLaunchKernelGGL((k_gemm_mfma<WT, 32>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || S == 1) return e;
+  return launch_splitk_epilogue(st, part, S, M, N, bias, epi, res, y);
+}
+
+template hipError_t launch_transpose<float>(hipStream_t, const float*, int, int, float*);
+template hipError_t launch_transpose<bf16_t>(hipStream_t, const bf16_t*, int, int, bf16_t*);
+template hipError_t launch_gemm_mfma<float>(hipStream_t, const float*, int, int, const float*, int, const float*, int,
+                                            const float*, float*, float*, size_t, int);
+template hipError_t launch_gemm_mfma<bf16_t>(hipStream_t, const float*, int, int, const bf16_t*, int, const float*,
+                                             int, const float*, float*, float*, size_t, int);
+
+}  // namespace fh

@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
   const int n = (int)(idx % N);
   float s = 0.f;
   for (int i = 0; i < S; i++) s += part[(size_t)i * M * N + idx];
-  s += bias[n];
+  if (bias) s += bias[n];
   if (epi == EPI_GELU) s = gelu_tanh(s);
   if (res) s += res[idx];
   y[idx] = s;
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void k_gemm_tiled(const float* __restrict__ A,
     for (int j = 0; j < 4; j++) {
       const int n = tn + tx * 4 + j;
       if (n >= N) continue;
-      float s = acc[i][j] + bias[n];
+      float s = acc[i][j] + (bias ? bias[n] : 0.f);
       if (epi == EPI_GELU) s = gelu_tanh(s);
       if (res) s += res[(size_t)m * N + n];
       Y[(size_t)m * N + n] = s;
@@ -752,7 +752,7 @@ hipError_t launch_gemv_splitk(hipStream_t st, const float* x, int M, int K, cons
 
 hipError_t launch_splitk_epilogue(hipStream_t st, const float* part, int splits, int M, int N, const float* bias,
                                   int epi, const float* res, float* y) {
-  FH_CHECK_ARG(splits >= 1 && M > 0 && N > 0 && part && bias && y);
+  FH_CHECK_ARG(splits >= 1 && M > 0 && N > 0 && part && y);
   const size_t tot = (size_t)M * N;
   hipLaunchKernelGGL(k_splitk_epilogue, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, part, splits, M, N,
                      bias, epi, res, y);
@@ -762,7 +762,7 @@ hipError_t launch_splitk_epilogue(hipStream_t st, const float* part, int splits,
 template <typename WT>
 hipError_t launch_gemm(hipStream_t st, const float* a, int M, int K, const WT* W, int N, const float* bias, int epi,
                        const float* res, float* y) {
-  FH_CHECK_ARG(M > 0 && K > 0 && N > 0 && a && W && bias && y);
+  FH_CHECK_ARG(M > 0 && K > 0 && N > 0 && a && W && y);
   dim3 grid((N + 63) / 64, (M + 63) / 64);
   hipLaunchKernelGGL(k_gemm_tiled<WT>, grid, dim3(256), 0, st, a, M, K, W, N, bias, epi, res, y);
   return hipGetLastError();

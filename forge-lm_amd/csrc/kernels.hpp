@@ -53,6 +53,17 @@ hipError_t launch_attn_decode(hipStream_t st, RowSrc src, const float* qkv, int 
 template <typename WT>
 hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* E, int V, float* logits);
 
+// MFMA GEMM (gemm_mfma.hip): y = epi(a[M,K] @ W + bias) (+ res) with W given
+// transposed as Wt[N][K]; K a multiple of 32.  Small M splits K over up to
+// part_floats of partials (then sums them with launch_splitk_epilogue).
+template <typename WT>
+hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, const float* bias,
+                            int epi, const float* res, float* y, float* part, size_t part_floats, int cus);
+
+// Wt[n][k] = W[k][n].
+template <typename WT>
+hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt);
+
 // dst[0..bytes) = src[0..bytes) on the device (both 16-byte aligned).
 hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);
 

@@ -27,7 +27,7 @@ FH_DTYPE_BF16 = 1
 EXPORTS = (
     "fh_last_error", "fh_version", "fh_random_doubles", "fh_context_create", "fh_context_destroy",
     "fh_context_info", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
-    "fh_buffer_copy",
+    "fh_buffer_copy", "fh_matmul_nn",
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_sample_logits",
@@ -83,6 +83,7 @@ def lib():
     L.fh_buffer_write.argtypes = [vp, vp, vp, ctypes.c_size_t]
     L.fh_buffer_read.argtypes = [vp, vp, vp, ctypes.c_size_t]
     L.fh_buffer_copy.argtypes = [vp, vp, vp, ctypes.c_size_t, P(ctypes.c_float)]
+    L.fh_matmul_nn.argtypes = [vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     L.fh_session_create.argtypes = [vp, P(ModelDesc), P(vp)]
     L.fh_session_destroy.argtypes = [vp]
     L.fh_param_count.argtypes = [P(ModelDesc)]

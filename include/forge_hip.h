@@ -108,6 +108,14 @@ int fh_buffer_read(fh_context* ctx, void* dst, const void* src_dev, size_t bytes
  * bandwidth calibration of the benchmark's traffic counters). */
 int fh_buffer_copy(fh_context* ctx, void* dst_dev, const void* src_dev, size_t bytes, float* ms_out);
 
+/* ITensorBackend.MatMulNN(a, b, y, M, K, N, accumulate) (ITensorBackend.cs:22) on
+ * device buffers: y[M][N] = a[M][K] @ b[K][N], or += when accumulate != 0.  a and
+ * y fp32; b fp32 or bf16 (dtype).  The product runs on the MFMA GEMM the token
+ * loop uses for more than 4 rows (bf16: a rounded to bf16, fp32 accumulation).
+ * Synchronous. */
+int fh_matmul_nn(fh_context* ctx, const void* a_dev, const void* b_dev, void* y_dev, int M, int K, int N,
+                 int dtype, int accumulate);
+
 /* session = weights + KV cache + token history + scratch for max_batch sequences */
 int fh_session_create(fh_context* ctx, const fh_model_desc* desc, fh_session** out);
 int fh_session_destroy(fh_session* s);

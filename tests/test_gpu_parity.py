@@ -207,3 +207,93 @@ def test_eos_stops_each_sequence(fhp, oracle, backend):
     out = fhp.Sampler.generate(m, [3, 1], 10, 0.0, 0, None, eos_id=first)
     assert list(out) == [first]
     m.dispose()
+
+
+# ---- MFMA GEMM (ITensorBackend.MatMulNN through fh_matmul_nn) --------------------------------
+
+def bf16_round(x):
+    """float32 -> nearest-even bfloat16, returned as float32 values and raw uint16 bits."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    u32 = u.astype(np.uint32)
+    return u32.view(np.float32), (u32 >> 16).astype(np.uint16)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 768, 2304), (32, 3072, 768), (300, 1024, 1000), (5, 64, 96),
+                                   (130, 96, 257), (7, 40, 33), (1, 32, 130)])
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_matmul_nn_matches_oracle(fhp, oracle, backend, M, K, N, dtype):
+    r = np.random.default_rng(M * 1000 + K + N)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    if dtype == "bf16":
+        a_used, _ = bf16_round(a) if K % 32 == 0 else (a, None)  # the MFMA path rounds a; the tiled one does not
+        b_used, b_bits = bf16_round(b)
+        b_dev_data = b_bits
+    else:
+        a_used, b_used, b_dev_data = a, b, b
+    bufa = fhp.DeviceBuffer.from_array(backend, a)
+    bufb = fhp.DeviceBuffer.from_array(backend, b_dev_data)
+    bufy = fhp.DeviceBuffer.from_array(backend, y0)
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=True, dtype=dtype)
+    got = bufy.read(np.float32, M * N).reshape(M, N)
+    ref = y0.astype(np.float64) + a_used.astype(np.float64) @ b_used.astype(np.float64)
+    # fp32 accumulation in another order than the reference's sequential k: bound
+    # the difference by the magnitude of the terms (|a| @ |b|)
+    scale = np.abs(a_used).astype(np.float64) @ np.abs(b_used).astype(np.float64) + np.abs(y0)
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-6), float(np.max(np.abs(got - ref) / (scale + 1e-6)))
+    # and against the oracle's own sequential fp32 MatMulNN (CpuBackend.cs:49-57)
+    if dtype == "f32":
+        exp = oracle.matmul_nn(a, b) + y0
+        assert np.all(np.abs(got - exp) <= 1e-5 * scale + 1e-6)
+    # without accumulate, y is overwritten
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=False, dtype=dtype)
+    got2 = bufy.read(np.float32, M * N).reshape(M, N)
+    assert np.all(np.abs(got2 - (ref - y0)) <= 1e-5 * scale + 1e-6)
+    for buf in (bufa, bufb, bufy):
+        buf.free()
+
+
+def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
+    # Forge-220M shape with bf16 weights (BASELINE config 5), reduced to a 64-token
+    # prompt and 3 steps per sequence so the CPU oracle stays quick; the oracle runs
+    # fp32 math on the same bf16-rounded parameters (north star: logits within 2e-2)
+    shape = (16384, 1024, 1024, 16, 16)
+    B, P, NEW = 2, 64, 3
+    ocfg = oracle.Config(*shape)
+    w = oracle.init_weights(ocfg, 1234)
+    wr = bf16_round(w)[0]  # every parameter carries bf16 precision in a bf16 session
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype="bf16")
+    m.load_weights(w)
+    r = fhp.TrainingRandom(42)
+    prompts = np.stack([r.ids(shape[0], P) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
+    oracle.set_threads(8)
+    for b in range(B):
+        rids, rlg = oracle.generate(ocfg, wr, prompts[b], NEW, return_logits=True)
+        assert rel_err(lg[b][0], rlg[0]) <= 2e-2
+        top2 = np.sort(rlg, axis=1)[:, -2:]
+        for n in range(NEW):
+            if top2[n, 1] - top2[n, 0] > 4e-2:  # ids must agree wherever the margin exceeds the tolerance
+                assert ids[b][n] == rids[n]
+            else:
+                break
+    m.dispose()
+
+
+def test_c4_shape_batched_decode_matches_oracle(fhp, oracle, backend):
+    # Forge-98M shape, 8 sequences decoded together (the batch-32 workload of
+    # BASELINE config 4 at a CPU-checkable size): every decode GEMM has M = 8
+    shape = (16384, 1024, 768, 12, 12)
+    B = 8
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234, batch=B)
+    r = fhp.TrainingRandom(7)
+    prompts = np.stack([r.ids(shape[0], 24) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, 6, 0.0, 0, None, return_logits=True)
+    oracle.set_threads(8)
+    for b in range(B):
+        rids, rlg = oracle.generate(oc, w, prompts[b], 6, return_logits=True)
+        np.testing.assert_array_equal(ids[b], rids)
+        assert rel_err(lg[b], rlg) <= TOL_F32
+    m.dispose()
