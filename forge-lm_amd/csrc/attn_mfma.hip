@@ -1,0 +1,245 @@
+// attn_mfma.hip -- causal prefill attention on MFMA for head_dim 64 (gfx950).
+//
+// MultiHeadAttention.Forward over a window (src/LLM.Core/Layers/Layers.cs:191-229,
+// ITensorBackend.cs:117-122): per head s = q.k * (1/sqrt(64)), keys past the
+// query masked, softmax, o = p @ v.  A block takes 128 queries of one
+// (sequence, head); each of its 4 waves owns 32 of them and walks the key tiles
+// (64 keys) up to its last query with an online softmax:
+//   S^T = K Q^T    MFMA with keys as rows: lane l holds query l % 32 and, in
+//                  element r, key (r/4)*8 + (l/32)*4 + r%4 of a 32-key half, so
+//                  the softmax statistics of a query stay inside its lane pair
+//   O^T += V^T P^T the score registers are the B operand as they are; V^T is
+//                  staged in LDS and read in the same key order.
+// bf16 sessions: v_mfma_f32_32x32x16_bf16 (q rounded to bf16, fp32 softmax and
+// accumulation); fp32 sessions: v_mfma_f32_32x32x2_f32 on exact fp32 values.
+#include "kernels.hpp"
+
+#include <math.h>
+
+#include <type_traits>
+
+namespace fh {
+
+namespace {
+
+constexpr int HD = 64;   // head dim
+constexpr int BQ = 128;  // queries per block (4 waves x 32)
+constexpr int BKV = 64;  // keys per tile
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
+
+__device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16(f)); }
+
+template <typename KT>
+__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restrict__ qkv, int T, int d, int H, int ctx,
+                                                          const KT* __restrict__ kc, const KT* __restrict__ vc,
+                                                          float* __restrict__ o) {
+  constexpr bool BF = sizeof(KT) == 2;
+  // K tile [key][dim] and V^T tile [dim][key]; fp32 K rows hold the even dims
+  // first, then the odd ones (float4 reads per half-wave)
+  constexpr int PAD = BF ? 8 : 4;
+  typedef typename std::conditional<BF, __bf16, float>::type E;
+  __shared__ __align__(16) E Ks[BKV][HD + PAD];
+  __shared__ __align__(16) E Vt[HD][BKV + PAD];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t0 = blockIdx.x * BQ, h = blockIdx.y, b = blockIdx.z;
+  const int qw0 = t0 + 32 * w;             // this wave's first query
+  const int q = qw0 + (lane & 31), half = lane >> 5;
+  const float scale = 0.125f;              // 1 / sqrt(64), exact
+  const KT* K = kc + ((size_t)b * H + h) * ctx * HD;
+  const KT* V = vc + ((size_t)b * H + h) * ctx * HD;
+
+  // this lane's q (row q, clamped for the loads)
+  const float* qrow = qkv + (size_t)(b * T + min(q, T - 1)) * 3 * d + h * HD;
+  bf16x8_t qb[4];                          // bf16: dims 16kk + 8*half .. +7
+  float qf[32];                            // fp32: dims 2s + half
+  if constexpr (BF) {
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * kk + 8 * half);
+      const float4 c = *reinterpret_cast<const float4*>(qrow + 16 * kk + 8 * half + 4);
+      qb[kk] = bf16x8_t{to_bf(a.x), to_bf(a.y), to_bf(a.z), to_bf(a.w), to_bf(c.x), to_bf(c.y), to_bf(c.z), to_bf(c.w)};
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float4 a = *reinterpret_cast<const float4*>(qrow + 4 * i);
+      qf[2 * i] = half ? a.y : a.x;
+      qf[2 * i + 1] = half ? a.w : a.z;
+    }
+  }
+
+  f32x16_t ot[2];  // O^T: dims (dt*32 + acc_row) x this lane's query
+#pragma unroll
+  for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) ot[dt][r] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  const int qlast = min(t0 + BQ, T) - 1;    // last query of the block
+  const int nkt = qlast / BKV + 1;
+  for (int kt = 0; kt < nkt; kt++) {
+    const int k0 = kt * BKV;
+    __syncthreads();  // the previous tile is consumed
+    // stage K and V^T (rows at or past T read as zeros)
+    if constexpr (BF) {
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int idx = tid + 256 * i, key = idx / 8, q8 = idx % 8;  // 8 x 8 bf16 per key row
+        uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = kv;
+        if (k0 + key < T) {
+          kv = *reinterpret_cast<const uint4*>(K + (size_t)(k0 + key) * HD + 8 * q8);
+          vv = *reinterpret_cast<const uint4*>(V + (size_t)(k0 + key) * HD + 8 * q8);
+        }
+        *reinterpret_cast<uint4*>(&Ks[key][8 * q8]) = kv;
+        const bf16_t* vh = reinterpret_cast<const bf16_t*>(&vv);
+#pragma unroll
+        for (int e = 0; e < 8; e++) Vt[8 * q8 + e][key] = __builtin_bit_cast(__bf16, vh[e]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int idx = tid + 256 * i, key = idx / 16, q4 = idx % 16;  // 16 x 4 floats per key row
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+        if (k0 + key < T) {
+          kv = *reinterpret_cast<const float4*>(K + (size_t)(k0 + key) * HD + 4 * q4);
+          vv = *reinterpret_cast<const float4*>(V + (size_t)(k0 + key) * HD + 4 * q4);
+        }
+        // dims 4q4 .. +3: even ones to 2q4, 2q4+1; odd ones to 32 + 2q4, +1
+        Ks[key][2 * q4] = kv.x;
+        Ks[key][2 * q4 + 1] = kv.z;
+        Ks[key][32 + 2 * q4] = kv.y;
+        Ks[key][32 + 2 * q4 + 1] = kv.w;
+        Vt[4 * q4 + 0][key] = vv.x;
+        Vt[4 * q4 + 1][key] = vv.y;
+        Vt[4 * q4 + 2][key] = vv.z;
+        Vt[4 * q4 + 3][key] = vv.w;
+      }
+    }
+    __syncthreads();
+    if (k0 > qw0 + 31 || qw0 >= T) continue;  // no query of this wave sees a key of the tile
+
+    // ---- S^T = K Q^T for the two 32-key halves ----
+    f32x16_t s[2];
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) s[jt][r] = 0.f;
+      const int kr = jt * 32 + (lane & 31);  // key row this lane supplies
+      if constexpr (BF) {
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Ks[kr][16 * kk + 8 * half]);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[kk], s[jt], 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+          const float4 a = *reinterpret_cast<const float4*>(&Ks[kr][32 * half + 4 * c]);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qf[4 * c + 0], s[jt], 0, 0, 0);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qf[4 * c + 1], s[jt], 0, 0, 0);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qf[4 * c + 2], s[jt], 0, 0, 0);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qf[4 * c + 3], s[jt], 0, 0, 0);
+        }
+      }
+    }
+    // ---- scale, causal mask, online softmax (per query = per lane pair) ----
+    float mt = -INFINITY;
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int key = k0 + jt * 32 + acc_row(lane, r);
+        const float v = (key <= q && key < T) ? s[jt][r] * scale : -INFINITY;
+        s[jt][r] = v;
+        mt = fmaxf(mt, v);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float mn = fmaxf(m, mt);
+    const float corr = (m == -INFINITY) ? 0.f : expf(m - mn);
+    float ls = 0.f;
+#pragma unroll
+    for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float p = (s[jt][r] == -INFINITY) ? 0.f : expf(s[jt][r] - mn);
+        s[jt][r] = p;
+        ls += p;
+      }
+    ls += __shfl_xor(ls, 32, 64);
+    l = l * corr + ls;
+    m = mn;
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) ot[dt][r] *= corr;
+
+    // ---- O^T += V^T P^T: a k step takes, per half-wave, the keys the score
+    // registers hold (keys 4*half + {0..3} and 8 + 4*half + {0..3} of 16) ----
+#pragma unroll
+    for (int dt = 0; dt < 2; dt++) {
+      const int vr = dt * 32 + (lane & 31);  // V^T row (dim) this lane supplies
+      if constexpr (BF) {
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+          for (int kk = 0; kk < 2; kk++) {
+            const int kb = jt * 32 + kk * 16 + 4 * half;
+            const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&Vt[vr][kb]);
+            const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&Vt[vr][kb + 8]);
+            const bf16x8_t a = bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            const int r0 = 8 * kk;
+            const bf16x8_t pb = bf16x8_t{to_bf(s[jt][r0 + 0]), to_bf(s[jt][r0 + 1]), to_bf(s[jt][r0 + 2]),
+                                         to_bf(s[jt][r0 + 3]), to_bf(s[jt][r0 + 4]), to_bf(s[jt][r0 + 5]),
+                                         to_bf(s[jt][r0 + 6]), to_bf(s[jt][r0 + 7])};
+            ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, ot[dt], 0, 0, 0);
+          }
+      } else {
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int key = jt * 32 + acc_row(lane, r);  // the key of score register r in this lane
+            ot[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vt[vr][key], s[jt][r], ot[dt], 0, 0, 0);
+          }
+      }
+    }
+  }
+
+  if (q >= T) return;
+  const float inv = 1.f / l;
+  float* orow = o + (size_t)(b * T + q) * d + h * HD;
+#pragma unroll
+  for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      // elements 4g .. 4g+3 are dims dt*32 + 8g + 4*half + 0..3
+      const float4 v = make_float4(ot[dt][4 * g] * inv, ot[dt][4 * g + 1] * inv, ot[dt][4 * g + 2] * inv,
+                                   ot[dt][4 * g + 3] * inv);
+      *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * half) = v;
+    }
+}
+
+}  // namespace
+
+template <typename KT>
+hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
+                                    const KT* kcache, const KT* vcache, float* o) {
+  if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !qkv || !kcache || !vcache || !o)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_prefill_mfma<KT>, dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, qkv, T, d, H, ctx,
+                     kcache, vcache, o);
+  return hipGetLastError();
+}
+
+template hipError_t launch_attn_prefill_mfma<float>(hipStream_t, const float*, int, int, int, int, int, const float*,
+                                                    const float*, float*);
+template hipError_t launch_attn_prefill_mfma<bf16_t>(hipStream_t, const float*, int, int, int, int, int,
+                                                     const bf16_t*, const bf16_t*, float*);
+
+}  // namespace fh

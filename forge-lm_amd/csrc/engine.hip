@@ -298,7 +298,10 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
     FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 2), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, T, D, H, C, kc, vc));
-    LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
+    if (D == 64 * H)
+      LAUNCH(launch_attn_prefill_mfma<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
+    else
+      LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
     FH_TRY(linear<WT>(s, s->o, M, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
     LAUNCH(launch_layernorm(st, s->x2, M, M, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
     FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,

@@ -43,6 +43,12 @@ template <typename KT>
 hipError_t launch_attn_prefill(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
                                const KT* kcache, const KT* vcache, float* o);
 
+// The same on MFMA tiles (attn_mfma.hip), for head_dim 64: bf16 caches multiply in bf16
+// (q and the softmax weights rounded to bf16), fp32 caches in fp32.
+template <typename KT>
+hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
+                                    const KT* kcache, const KT* vcache, float* o);
+
 // Decode attention of one row per sequence over keys 0..pos (pos from src), split over
 // chunks of `chunk` keys, then combined.  part must hold B*H*max_chunks*(hd+2) floats.
 template <typename KT>

@@ -297,3 +297,34 @@ def test_c4_shape_batched_decode_matches_oracle(fhp, oracle, backend):
         np.testing.assert_array_equal(ids[b], rids)
         assert rel_err(lg[b], rlg) <= TOL_F32
     m.dispose()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_head_dim_64_window_prefill_matches_oracle(fhp, oracle, backend, dtype):
+    # head_dim 64 runs prefill attention on MFMA tiles of 128 queries x 64 keys:
+    # windows of 1, 64, 127, 129 and 200 rows cover single, partial and ragged
+    # tiles; a 200-row window past a 160-token context re-prefills every step
+    shape = (512, 160, 128, 2, 2)
+    ocfg = oracle.Config(*shape)
+    w = oracle.init_weights(ocfg, 99)
+    wref = bf16_round(w)[0] if dtype == "bf16" else w
+    tol = 2e-2 if dtype == "bf16" else TOL_F32
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=2, dtype=dtype)
+    m.load_weights(w)
+    r = fhp.TrainingRandom(3)
+    for T in (1, 64, 127, 129, 160):
+        ids = np.stack([r.ids(shape[0], T), r.ids(shape[0], T)])
+        out = m.forward_last(ids)
+        for b in range(2):
+            assert rel_err(out[b], oracle.forward(ocfg, wref, ids[b])[-1]) <= tol, (T, b)
+    prompts = np.stack([r.ids(shape[0], 150), r.ids(shape[0], 150)])
+    ids, lg = fhp.Sampler.generate(m, prompts, 20, 0.0, 0, None, return_logits=True)
+    for b in range(2):
+        rids, rlg = oracle.generate(ocfg, wref, prompts[b], 20, return_logits=True)
+        top2 = np.sort(rlg, axis=1)[:, -2:]
+        for n in range(20):
+            assert rel_err(lg[b][n], rlg[n]) <= tol, (b, n)
+            if top2[n, 1] - top2[n, 0] <= 2 * tol:  # a near tie may flip; later steps then differ
+                break
+            assert ids[b][n] == rids[n], (b, n)
+    m.dispose()
