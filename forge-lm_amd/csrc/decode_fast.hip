@@ -69,8 +69,8 @@ __device__ __forceinline__ bool err_set(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
 // The first failing wait records where it was: 1 << 31 | wait << 24 | layer << 16 | block
-// (waits: 1 x, 2 q/k/v, 3 attention partials, 4 o, 5 attn.proj partials, 6 x2, 7 h,
-// 8 mlp.proj partials, 9 final x, 10 argmax).
+// (waits: 1 x, 2 q/k/v, 3 attention partials, 5 attn.proj partials, 6 x2, 7 h,
+// 8 mlp.proj partials, 9 final x, 10 argmax; 4 is not used).
 // A wait that gives up because another block already failed records nothing.
 enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX };
 __device__ __forceinline__ int err_code(int wait, int l) {
@@ -104,15 +104,21 @@ __device__ __forceinline__ unsigned xcc_id() {
 // stores (plain loads would keep hitting a stale L1 line).  Out-of-range
 // offsets read as 0.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-struct NcBuf {
+template <int AUX>
+struct NcBufT {
   __amdgpu_buffer_rsrc_t r;
-  __device__ NcBuf(const void* base, int bytes)
+  __device__ NcBufT(const void* base, int bytes)
       : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000)) {}
   __device__ __forceinline__ uint4 load4(int byte_off) const {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 17);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, AUX);
     return make_uint4(v.x, v.y, v.z, v.w);
   }
 };
+#ifndef FH_LOCAL_AUX
+#define FH_LOCAL_AUX 17
+#endif
+using NcBuf = NcBufT<17>;            // uncached (cross-XCD) hand-offs
+using LcBuf = NcBufT<FH_LOCAL_AUX>;  // XCD-local hand-offs
 
 template <int D, int H>
 struct Shape {
@@ -135,8 +141,6 @@ struct Shape {
   static constexpr size_t QT = (size_t)QCMAX * D, PT = (size_t)PJ * NDW * G * 256, FT = (size_t)FCOL * D,
                           MT = (size_t)NDW * G * MJ * 256;
   static constexpr size_t LAYER = (size_t)NB * (QT + PT + FT + MT);
-  // compact vector buffer per layer: ln1.w ln1.b ln2.w ln2.b
-  static constexpr int V_LN1W = 0, V_LN1B = D, V_LN2W = 2 * D, V_LN2B = 3 * D, VL = 4 * D;
   // per-block bias table per layer: qkv[QCMAX] fc[FCOL] proj[RSC] mproj[RSC]
   static constexpr int B_Q = 0, B_F = QCMAX, B_P = QCMAX + FCOL, B_M = QCMAX + FCOL + RSC,
                        BT = QCMAX + FCOL + 2 * RSC;
@@ -157,8 +161,7 @@ struct Xl {
   using S = Shape<D, H>;
   static constexpr int QKV = 0;                                   // q, k, v of the XCD's heads
   static constexpr int PARTS = QKV + 3 * S::HD * S::HPX;          // attention partials
-  static constexpr int O = PARTS + S::HPX * S::SPH * PART;        // o of the XCD's heads
-  static constexpr int X2 = O + S::HD * S::HPX;                   // x2 (every XCD keeps a copy)
+  static constexpr int X2 = PARTS + S::HPX * S::SPH * PART;       // x2 (every XCD keeps a copy)
   static constexpr int HH = X2 + D;                               // the XCD's h slice
   static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
   static constexpr int STRIDE = X + D;
@@ -167,7 +170,7 @@ struct Xl {
 struct KParams {
   RowSrc src;
   const float* tiles;
-  const float* vecs;
+  const float* vecs;  // ln_f weight, bias
   const float* btab;
   const float* tok;
   const float* pos;
@@ -195,16 +198,19 @@ constexpr int TRACE_PER = 32;
 __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
   if (t && threadIdx.x == (NT - 64)) t[blockIdx.x * TRACE_PER + i] = wall_clock64();
 }
-__device__ __forceinline__ void trace_mark_d(unsigned long long* t, int i) {
-  if (t && threadIdx.x == 0) t[blockIdx.x * TRACE_PER + 16 + i] = wall_clock64();
+// data wave 0 keeps its marks in LDS (a global store would make its next
+// wait for a tile cover every load in flight); the control wave writes them out
+__device__ __forceinline__ void trace_mark_d(unsigned long long* t, unsigned long long* lds, int i) {
+  if (t && threadIdx.x == 0) lds[i] = wall_clock64();
 }
 
 // Control wave: waits until pairs[pair0, pair0 + n) all carry `tag` (n <= N),
 // then stores the values to out[0, n) (LDS).  One read in flight: a second poll
 // issued ahead would still be in flight when the wait ends, and reusing its
 // registers would wait for it.
-template <int N>
-__device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int* err, int code, int n = N) {
+template <int N, typename B>
+__device__ bool gather(const B& nc, int pair0, unsigned tag, float* out, int* err, int code, int n = N,
+                       long* npoll = nullptr) {
   static_assert(N % 2 == 0, "pairs come in 16-byte loads");
   constexpr int R = (N + 127) / 128;
   const int lane = threadIdx.x & 63;
@@ -224,6 +230,7 @@ __device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int
       return false;
     }
   }
+  if (npoll) *npoll = it;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int i = 2 * (r * 64 + lane);
@@ -235,7 +242,8 @@ __device__ bool gather(const NcBuf& nc, int pair0, unsigned tag, float* out, int
 // Control wave: the RSC-column slice [slot*RSC, +RSC) of all NX per-XCD partial
 // vectors (pairs at pair0 + x*D + c), into out[x*RSC + c] (LDS).
 template <int D, int RSC>
-__device__ bool gather_slices(const NcBuf& nc, int pair0, int slot, unsigned tag, float* out, int* err, int code) {
+__device__ bool gather_slices(const NcBuf& nc, int pair0, int slot, unsigned tag, float* out, int* err, int code,
+                              long* npoll = nullptr) {
   constexpr int Q = RSC / 2;  // 16-byte loads per slice
   constexpr int NQ = NX * Q;
   constexpr int R = (NQ + 63) / 64;
@@ -258,6 +266,7 @@ __device__ bool gather_slices(const NcBuf& nc, int pair0, int slot, unsigned tag
       return false;
     }
   }
+  if (npoll) *npoll = it;
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const int u = r * 64 + lane;
@@ -335,391 +344,475 @@ __device__ __forceinline__ void load_chunks(float4 (&r)[N], const float* tile, b
   for (int i = 0; i < N; i++) r[i] = ld4(rs, off + i * 1024);
 }
 
+// LayerNorm statistics of xin[D] (LDS) for this lane's elements k = c*256 +
+// lane*4 + 0..3: d = x - mu, returns rs = 1 / sqrt(var + 1e-5) (biased
+// variance, CpuBackend.LayerNormForward).  The LayerNorm weight is folded into
+// the tiles and its bias into the bias table, so a column is rs * (d . W') + c.
+template <int KC, int D>
+__device__ __forceinline__ float ln_center(const float* xin, float4 (&d)[KC]) {
+  const int lane = threadIdx.x & 63;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < KC; c++) {
+    d[c] = *reinterpret_cast<const float4*>(xin + c * 256 + lane * 4);
+    s += (d[c].x + d[c].y) + (d[c].z + d[c].w);
+  }
+  const float mu = wave_sum_dpp(s) / (float)D;
+  float v = 0.f;
+#pragma unroll
+  for (int c = 0; c < KC; c++) {
+    d[c].x -= mu;
+    d[c].y -= mu;
+    d[c].z -= mu;
+    d[c].w -= mu;
+    v += (d[c].x * d[c].x + d[c].y * d[c].y) + (d[c].z * d[c].z + d[c].w * d[c].w);
+  }
+  const float var = wave_sum_dpp(v);
+  return 1.f / sqrtf(var / (float)D + 1e-5f);
+}
+
+// Control wave: the attention partials of the XCD's nh heads, nkb key blocks
+// each (pairs at pair0 + (j * SPH + kb) * PART + e), into out[(j * SPH + kb) * PART + e].
+// RA = loads per lane (ceil(n / 64)) is a template parameter so that every
+// load of a poll is issued before the first wait.
+template <int D, int H, int RA, typename B>
+__device__ bool gather_parts_r(const B& nc, int pair0, int nh, int nkb, unsigned tag, float* out, int* err, int code,
+                               long* npoll, unsigned long long* tfirst) {
+  using S = Shape<D, H>;
+  constexpr int Q = PART / 2;  // 16-byte loads per partial
+  const int lane = threadIdx.x & 63;
+  const int per = nkb * Q, n = nh * per;
+  // byte offset of each of this lane's loads (clamped into range; the extra
+  // lanes re-read the last unit and are not checked)
+  int off[RA];
+#pragma unroll
+  for (int i = 0; i < RA; i++) {
+    const int u = min(i * 64 + lane, n - 1), j = u / per, q = u - j * per;
+    off[i] = (pair0 + j * S::SPH * PART + 2 * q) * 8;
+  }
+  uint4 v[RA];
+  long it = 0;
+  for (;;) {
+    reload_fence();
+#pragma unroll
+    for (int i = 0; i < RA; i++) v[i] = nc.load4(off[i]);
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < RA; i++)
+      if (i * 64 + lane < n) ok &= (v[i].y == tag) & (v[i].w == tag);
+    if (tfirst && it == 0) *tfirst = wall_clock64();
+    if (__all(ok)) break;
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
+      return false;
+    }
+  }
+  if (npoll) *npoll = it;
+#pragma unroll
+  for (int i = 0; i < RA; i++) {
+    const int u = i * 64 + lane;
+    if (u < n) {
+      const int j = u / per, q = u - j * per;
+      *reinterpret_cast<float2*>(out + j * S::SPH * PART + 2 * q) =
+          make_float2(__uint_as_float(v[i].x), __uint_as_float(v[i].z));
+    }
+  }
+  return true;
+}
+
+template <int D, int H, typename B>
+__device__ bool gather_parts(const B& nc, int pair0, int nh, int nkb, unsigned tag, float* out, int* err, int code,
+                             long* npoll = nullptr, unsigned long long* tfirst = nullptr) {
+  using S = Shape<D, H>;
+  static_assert((S::HPX * S::SPH * PART / 2 + 63) / 64 <= 17, "partial loads per lane");
+  const int ra = (nh * nkb * (PART / 2) + 63) / 64;
+#define FH_PARTS_CASE(k) \
+  case k:                \
+    return gather_parts_r<D, H, k>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
+  switch (ra) {
+    FH_PARTS_CASE(1)
+    FH_PARTS_CASE(2)
+    FH_PARTS_CASE(3)
+    FH_PARTS_CASE(4)
+    FH_PARTS_CASE(5)
+    FH_PARTS_CASE(6)
+    FH_PARTS_CASE(7)
+    FH_PARTS_CASE(8)
+    FH_PARTS_CASE(9)
+    FH_PARTS_CASE(10)
+    FH_PARTS_CASE(11)
+    FH_PARTS_CASE(12)
+    FH_PARTS_CASE(13)
+    FH_PARTS_CASE(14)
+    FH_PARTS_CASE(15)
+    FH_PARTS_CASE(16)
+    default:
+      return gather_parts_r<D, H, 17>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
+  }
+#undef FH_PARTS_CASE
+}
+
+// LDS of one block
 template <int D, int H>
-__global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
+struct Lds {
+  using S = Shape<D, H>;
+  __align__(16) float xres[D];
+  __align__(16) float x2s[D];
+  __align__(16) float os[S::HD * S::HPX];              // o of the XCD's heads
+  __align__(16) float hs[S::HX];                       // the XCD's h slice
+  __align__(16) float rsv[NX * S::RSC];                // this slot's columns of the per-XCD partials
+  __align__(16) float qkvs[192];                       // this head's q, new k, new v
+  __align__(16) float wo[NW][64];                      // per-wave attention partials
+  __align__(16) float parts[S::HPX * S::SPH * PART];  // attention partials of the XCD's heads
+  float pw[64];                                        // their weights in the combination
+  float wm[NW], wl[NW];
+  float bias_s[2][S::BT];
+  float hval[S::RMAX];
+  unsigned long long trd[16];  // data wave 0's trace marks (0..13)
+  int fail;
+};
+
+// What this block and wave do in the step
+struct Role {
+  int blk, w, lane, xcd, slot, vb;
+  int nh, qc, qcw;      // heads of the XCD; qkv columns of the block and of a data wave
+  int hj, kb, ah;       // attention: local head, key block, global head
+  int pos, nk, nkb;     // new position, keys, key blocks per head
+  int key0;             // this data wave's first key
+  bool wave_keys;
+  unsigned tagbase;
+  uint2* xl;            // this XCD's local pairs
+  int xl0;              // same, as a pair index into p.xl
+};
+
+// Control wave: collects every hand-off.  ATTN: this block computes attention
+// (it gathers its head's q/k/v and publishes the block's partial).  After a
+// failed wait (sh.fail) it skips the remaining waits and stores but meets
+// every barrier: the loops have no early exit, which keeps the compiler's
+// load-wait bookkeeping exact across iterations.
+template <int D, int H, bool ATTN>
+__device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const Role& r) {
   using S = Shape<D, H>;
   using U = Xu<D>;
   using XL = Xl<D, H>;
-  constexpr int KC = S::KC, RSC = S::RSC, G = S::G;
-  __shared__ __align__(16) float xres[D];
-  __shared__ __align__(16) float x2s[D];
-  __shared__ __align__(16) float os[S::HD * S::HPX];  // o of the XCD's heads
-  __shared__ __align__(16) float hs[S::HX];           // the XCD's h slice
-  __shared__ __align__(16) float rsv[NX * RSC];       // this slot's columns of the per-XCD partials
-  __shared__ __align__(16) float qkvs[192];           // this head's q, new k, new v
-  __shared__ __align__(16) float wo[NW][64];
-  __shared__ float wm[NW], wl[NW];
-  __shared__ __align__(16) float aph[S::SPH][PART];  // partials of the head's other blocks (combiner)
-  __shared__ float bias_s[2][S::BT];
-  __shared__ float hval[S::RMAX];
-  __shared__ int fail_s;
-
-  // w is wave-uniform; readfirstlane lets the compiler know, so buffer
-  // resources built from it stay in scalar registers
-  const int blk = blockIdx.x, tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const bool ctrl = w == NW - 1;
-  // The dispatcher deals consecutive blocks to consecutive XCDs, continuing
-  // from wherever the previous dispatch stopped: the XCD comes from the
-  // hardware, and blocks b = 8k .. 8k+7 (slot k) land on 8 different XCDs.
-  const int xcd = (int)xcc_id() & (NX - 1), slot = blk / NX;
-  // every tile and bias depends on (XCD, slot): they are stored under the
-  // virtual block id vb; the head rows are indexed by blk
-  const int vb = slot * NX + xcd;
-  if (tid == 0) fail_s = 0;
-  const unsigned tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
-  trace_mark(p.trace, 30);
-
-  const int n = *p.src.step;
-  const int pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token (>= 1)
-  int tokid = p.src.tokens[p.src.tok_off + n];
-  if ((unsigned)tokid >= (unsigned)p.V) tokid = 0;
-  const int ctx = p.ctx;
-  uint2* const xl = p.xl + (size_t)xcd * XL::STRIDE;  // this XCD's local pairs
-  const int xl0 = xcd * XL::STRIDE;                   // same, as a pair index into p.xl
-
-  // qkv columns: the XCD's heads h = xcd + 8j (j < nh) own columns
-  // [j*192, j*192+192) of the XCD's list (q, k, v of each head); slot s has qc of them
-  const int nh = (H - xcd + NX - 1) / NX;
-  const int qc = 3 * S::HD * nh / SLOTS, qcw = qc / NDW;
-  // attention role: local head hj = slot / SPH, key block kb = slot % SPH
-  const int hj = slot / S::SPH, kb = slot % S::SPH;
-  const int ah = xcd + NX * hj;
-  const int nk = pos + 1, nkb = (nk + KPB - 1) / KPB;
-  const bool attn_blk = hj < nh && kb < nkb;
-
-  // x = tok_emb[id] + pos_emb[pos] (every block keeps its own copy)
-  for (int i = tid; i < D; i += NT) xres[i] = p.tok[(size_t)tokid * D + i] + p.pos[(size_t)pos * D + i];
-
-  // The control wave and the data waves run separate loops that meet at the
-  // same sequence of barriers; each barrier that follows a wait is followed
-  // by a check of fail_s in both loops.
-  bool ok = true;
-#define SYNC_OK()  \
-  __syncthreads(); \
-  if (fail_s) {    \
-    ok = false;    \
-    break;         \
-  }
-  if (ctrl) {
-    // ================= control wave: collects every hand-off =================
-    const NcBuf ncu(p.uc, p.uc_bytes), ncl(p.xl, p.xl_bytes);
+  constexpr int RSC = S::RSC;
+  const int lane = r.lane;
+  const NcBuf ncu(p.uc, p.uc_bytes);
+  const LcBuf ncl(p.xl, p.xl_bytes);
+  bool dead = false;
+  long np[7] = {0, 0, 0, 0, 0, 0, 0};  // polls per gather (trace)
+  unsigned long long tfirst = 0, tvis = 0, tdone = 0;
+  auto fail = [&]() {
+    dead = true;
+    sh.fail = 1;
+  };
 #define TM(i) \
   if (l == 1) trace_mark(p.trace, (i))
-    for (int l = 0; l < p.L; l++) {
-      const unsigned tb = tagbase + PH * l;
-      const unsigned tA = tb, tP = tb + 1, tB = tb + 2, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6,
-                     tE2 = tb + 7;
-      // ---- A: x of this layer (every XCD's copy) ----
-      for (int i = lane; i < S::BT; i += 64) bias_s[l & 1][i] = p.btab[((size_t)l * NB + vb) * S::BT + i];
-      if (l > 0 && !gather<D>(ncl, xl0 + XL::X, tb - PH + 7, xres, p.err, err_code(W_X, l))) fail_s = 1;
-      SYNC_OK();
-      TM(0);
-      // ---- B: attention ----
-      if (attn_blk) {
-        if (!gather<192>(ncl, xl0 + XL::QKV + hj * 192, tA, qkvs, p.err, err_code(W_QKV, l))) fail_s = 1;
-        SYNC_OK();
-        TM(1);
-        __syncthreads();  // the data waves' partials are in wm / wl / wo
-        float M = -INFINITY;
+  for (int l = 0; l < p.L; l++) {
+    const unsigned tb = r.tagbase + PH * l;
+    const unsigned tA = tb, tP = tb + 1, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6, tE2 = tb + 7;
+    // ---- A: x of this layer (every XCD's copy) ----
+    for (int i = lane; i < S::BT; i += 64) sh.bias_s[l & 1][i] = p.btab[((size_t)l * NB + r.vb) * S::BT + i];
+    if (l > 0 && !dead && !gather<D>(ncl, r.xl0 + XL::X, tb - PH + 7, sh.xres, p.err, err_code(W_X, l), D, &np[0]))
+      fail();
+    __syncthreads();
+    TM(0);
+    if (l == 2) trace_mark(p.trace, 9);
+    // Every phase whose data waves publish and then request tiles has a
+    // second barrier between the two, so that no published value queues
+    // behind the tile loads of another wave of this CU.
+    __syncthreads();
+    // ---- B: attention of this block's keys; publish the block's partial ----
+    if constexpr (ATTN) {
+      if (!dead && !gather<192>(ncl, r.xl0 + XL::QKV + r.hj * 192, tA, sh.qkvs, p.err, err_code(W_QKV, l), 192,
+                                &np[1]))
+        fail();
+      __syncthreads();
+      TM(1);
+      __syncthreads();  // the data waves' partials are in wm / wl / wo
+      float M = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < NDW; i++) M = fmaxf(M, wm[i]);
-        float Ls = 0.f, o = 0.f;
+      for (int i = 0; i < NDW; i++) M = fmaxf(M, sh.wm[i]);
+      float Ls = 0.f, o = 0.f;
 #pragma unroll
-        for (int i = 0; i < NDW; i++) {
-          const float f = (wm[i] == -INFINITY) ? 0.f : expf(wm[i] - M);
-          Ls += wl[i] * f;
-          o += wo[i][lane] * f;
-        }
-        if (nkb == 1) {
-          put_pair(xl + XL::O + hj * 64 + lane, o / Ls, tB);
-        } else if (kb > 0) {
-          uint2* pp = xl + XL::PARTS + (hj * S::SPH + kb) * PART;
-          put_pair(pp + lane, o, tP);
-          if (lane < PART - 64) put_pair(pp + 64 + lane, lane == 0 ? M : (lane == 1 ? Ls : 0.f), tP);
-        } else {
-          // combiner: the head's other key blocks' partials
-          constexpr int Q = PART / 2;  // 16-byte loads per partial
-          constexpr int RM = ((S::SPH - 1) * Q + 63) / 64;
-          const int nload = (nkb - 1) * Q;
-          const int pbase = (xl0 + XL::PARTS + hj * S::SPH * PART + PART) * 8;  // partial kb = 1
-          uint4 v[RM];
-          long it = 0;
-          bool good = true;
-          for (;;) {
-            reload_fence();
-#pragma unroll
-            for (int r = 0; r < RM; r++) v[r] = ncl.load4(pbase + (r * 64 + lane) * 16);
-            bool okk = true;
-#pragma unroll
-            for (int r = 0; r < RM; r++)
-              if (r * 64 + lane < nload) okk &= (v[r].y == tP) & (v[r].w == tP);
-            if (__all(okk)) break;
-            if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
-              if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_PART, l));
-              good = false;
-              break;
-            }
-          }
-          if (good) {
-            float* a = &aph[0][0];
-#pragma unroll
-            for (int r = 0; r < RM; r++) {
-              const int q = r * 64 + lane;
-              if (q < nload)
-                *reinterpret_cast<float2*>(a + 2 * q) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
-            }
-            wave_lds_sync();
-            float M2 = M;
-            for (int c = 0; c < nkb - 1; c++) M2 = fmaxf(M2, aph[c][64]);
-            float f = expf(M - M2);
-            float L2 = Ls * f, o2 = o * f;
-            for (int c = 0; c < nkb - 1; c++) {
-              f = expf(aph[c][64] - M2);
-              L2 += aph[c][65] * f;
-              o2 += aph[c][lane] * f;
-            }
-            put_pair(xl + XL::O + hj * 64 + lane, o2 / L2, tB);
-          } else {
-            fail_s = 1;
-          }
-        }
+      for (int i = 0; i < NDW; i++) {
+        const float f = (sh.wm[i] == -INFINITY) ? 0.f : expf(sh.wm[i] - M);
+        Ls += sh.wl[i] * f;
+        o += sh.wo[i][lane] * f;
+      }
+      if (!dead) {
+        uint2* pp = r.xl + XL::PARTS + (r.hj * S::SPH + r.kb) * PART;
+        put_pair(pp + lane, o, tP);
+        if (lane < PART - 64) put_pair(pp + 64 + lane, lane == 0 ? M : (lane == 1 ? Ls : 0.f), tP);
       }
       TM(2);
-      // ---- C: o of the XCD's heads ----
-      if (!gather<S::HD * S::HPX>(ncl, xl0 + XL::O, tB, os, p.err, err_code(W_O, l), S::HD * nh)) fail_s = 1;
-      SYNC_OK();
-      TM(3);
-      // ---- x2 = x + attn.proj(o) + b: this slot's columns from the 8 XCD partials ----
-      if (!gather_slices<D, RSC>(ncu, U::PX2, slot, tC, rsv, p.err, err_code(W_PX2, l))) fail_s = 1;
-      TM(7);
-      wave_lds_sync();
-      if (lane < RSC) {
-        float sum = 0.f;
-#pragma unroll
-        for (int x = 0; x < NX; x++) sum += rsv[x * RSC + lane];
-        const int col = slot * RSC + lane;
-        put_pair(xl + XL::X2 + col, (sum + bias_s[l & 1][S::B_P + lane]) + xres[col], tC2);
+      if (l == 1 && p.trace) {  // trace: when this block's own partial reads back
+        const int pb = (r.xl0 + XL::PARTS + (r.hj * S::SPH + r.kb) * PART) * 8;
+        for (long it = 0; it < SPIN_LIMIT; it++) {
+          reload_fence();
+          const uint4 v = ncl.load4(pb + lane * 16);
+          if (__all(lane >= PART / 2 || (v.y == tP && v.w == tP))) break;
+        }
+        tvis = wall_clock64();
       }
-      if (!gather<D>(ncl, xl0 + XL::X2, tC2, x2s, p.err, err_code(W_X2, l))) fail_s = 1;
-      SYNC_OK();
-      TM(4);
-      // ---- D: the XCD's h slice ----
-      if (!gather<S::HX>(ncl, xl0 + XL::HH, tD, hs, p.err, err_code(W_H, l))) fail_s = 1;
-      SYNC_OK();
-      TM(5);
-      // ---- E: x = x2 + mlp.proj(h) + b: this slot's columns from the 8 XCD partials ----
-      if (!gather_slices<D, RSC>(ncu, U::PX, slot, tE, rsv, p.err, err_code(W_PX, l))) fail_s = 1;
-      TM(8);
-      wave_lds_sync();
-      if (lane < RSC) {
-        float sum = 0.f;
-#pragma unroll
-        for (int x = 0; x < NX; x++) sum += rsv[x * RSC + lane];
-        const int col = slot * RSC + lane;
-        put_pair(xl + XL::X + col, (sum + bias_s[l & 1][S::B_M + lane]) + x2s[col], tE2);
-      }
-      TM(6);
+      __syncthreads();  // the partial is published before the data waves request K/V
     }
-#undef TM
-    if (ok) {
-      // ---- head ----
-      if (!gather<D>(ncl, xl0 + XL::X, tagbase + PH * (p.L - 1) + 7, xres, p.err, err_code(W_XF, 0))) fail_s = 1;
-      __syncthreads();
-      ok = !fail_s;
-      if (ok) {
-        __syncthreads();  // hval holds this block's logits
-        // block 0 collects every block's argmax: it proves all blocks read this
-        // launch's counter, so the counter can advance
-        const unsigned tH = tagbase + PH * p.L;
-        if (blk == 0) {
-          float best = -INFINITY;
-          int bi = 0x7fffffff;
-          long it = 0;
-          bool good = true;
-          for (;;) {
-            reload_fence();
-            bool okk = true;
-            best = -INFINITY;
-            bi = 0x7fffffff;
+    // ---- C: o of the XCD's heads from every key block's partial ----
+    if (!dead &&
+        !gather_parts<D, H>(ncl, r.xl0 + XL::PARTS, r.nh, r.nkb, tP, sh.parts, p.err, err_code(W_PART, l), &np[2],
+                            (l == 1 && p.trace) ? &tfirst : nullptr))
+      fail();
+    if (l == 1 && p.trace) tdone = wall_clock64();
+    if (!dead) {
+      // lane t < nh * nkb holds partial (j, c) = (t / nkb, t % nkb): its weight
+      // exp(m - M_j) goes to sh.pw; then lane d sums o[d] over the head's partials
+      wave_lds_sync();
+      const int np = r.nh * r.nkb, jt = lane / r.nkb, ct = lane - jt * r.nkb;
+      const bool has = lane < np;
+      const float mt = has ? sh.parts[(jt * S::SPH + ct) * PART + 64] : -INFINITY;
+      const float lt = has ? sh.parts[(jt * S::SPH + ct) * PART + 65] : 0.f;
+      float Lj[S::HPX];
 #pragma unroll
-            for (int r = 0; r < NB / 64; r++) {
-              const uint4 a = ncu.load4(p.off_amax + 16 * (r * 64 + lane));
-              okk &= a.z == tH;
-              argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
-            }
-            if (__all(okk)) break;
-            if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
-              if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_AMAX, 0));
-              good = false;
-              break;
-            }
-          }
-          if (good) {
-            wave_argmax(best, bi);
-            if (lane == 0) {
-              if (p.greedy) {
-                const int total = p.src.tok_off + 1 + n;  // prompt_len + n
-                p.tokens_out[total] = bi;
-                if (n < p.max_new) p.out_ids[n] = bi;
-                if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
-                *p.step_out = n + 1;
-              }
-              __hip_atomic_fetch_add(p.launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-          }
+      for (int j = 0; j < S::HPX; j++) {
+        const float Mj = wave_max_dpp(has && jt == j ? mt : -INFINITY);
+        const float f = (has && jt == j) ? expf(mt - Mj) : 0.f;
+        Lj[j] = wave_sum_dpp(lt * f);
+        if (has && jt == j) sh.pw[lane] = f;
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int j = 0; j < S::HPX; j++) {
+        if (j < r.nh) {
+          const float* pj = sh.parts + j * S::SPH * PART;
+          float o = 0.f;
+          for (int c = 0; c < r.nkb; c++) o += pj[c * PART + lane] * sh.pw[j * r.nkb + c];
+          sh.os[j * 64 + lane] = o / Lj[j];
         }
       }
     }
-  } else {
-    // ================= data waves: weights in registers =================
-    const int key0 = kb * KPB + w * KPW;  // this data wave's first key
-    const bool wave_keys = attn_blk && key0 < nk;
-    // Register tiles, each requested at least two phases before its use;
-    // every register is loaded on every path (an empty buffer resource when
-    // there is nothing to fetch), so none stays live across the whole loop:
-    //   attention blocks   A: rf(l), LN2(l)  B: rm(l)  C: rq(l+1)  D: LN1(l+1)  E: rp(l+1), K/V(l+1)
-    //   the others         A: rf(l), LN2(l), rm(l), rq(l+1)  C: rp(l+1)  D: LN1(l+1)
-    float4 rq[S::QCW * KC], rp[S::PJ * G], rf[S::FCW * KC], rm[G * S::MJ];
-    // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
-    // lane l the dims 4*(l % 16) .. +3 of row key0 + 4i + l / 16 (one 1 KB load each)
-    float4 kr[KPW / 4], vr[KPW / 4];
-    float4 lnw[KC], lnb[KC];  // this lane's LayerNorm parameters: LN1(l) until A, LN2(l) until D
-    auto load_ln = [&](const float* wv, const float* bv) {
-      const __amdgpu_buffer_rsrc_t rw = make_rsrc(wv, D * 4), rb = make_rsrc(bv, D * 4);
+    __syncthreads();
+    TM(3);
+    __syncthreads();
+    // ---- x2 = x + attn.proj(o) + b: this slot's columns from the 8 XCD partials ----
+    if (!dead && !gather_slices<D, RSC>(ncu, U::PX2, r.slot, tC, sh.rsv, p.err, err_code(W_PX2, l), &np[3])) fail();
+    TM(7);
+    wave_lds_sync();
+    if (!dead && lane < RSC) {
+      float sum = 0.f;
 #pragma unroll
-      for (int c = 0; c < KC; c++) {
-        lnw[c] = ld4(rw, c * 1024 + lane * 16);
-        lnb[c] = ld4(rb, c * 1024 + lane * 16);
-      }
-    };
-    auto tile = [&](int l) { return p.tiles + (size_t)l * S::LAYER; };
-    // qkv: a block with qcw < QCW columns per wave reads its chunks twice (same
-    // addresses, no extra HBM bytes) so the loads stay unconditional
-    auto load_q = [&](int l, bool real) {
-      constexpr int HALF = S::QCW * KC / 2;
-      const float* t = tile(l) + (size_t)vb * S::QT + (size_t)w * qcw * D;
-      const __amdgpu_buffer_rsrc_t lo = make_rsrc(t, real ? HALF * 1024 : 0);
-      const __amdgpu_buffer_rsrc_t hi = make_rsrc(qcw == S::QCW ? t + HALF * 256 : t, real ? HALF * 1024 : 0);
-      const int off = lane * 16;
+      for (int x = 0; x < NX; x++) sum += sh.rsv[x * RSC + lane];
+      const int col = r.slot * RSC + lane;
+      put_pair(r.xl + XL::X2 + col, (sum + sh.bias_s[l & 1][S::B_P + lane]) + sh.xres[col], tC2);
+    }
+    if (!dead && !gather<D>(ncl, r.xl0 + XL::X2, tC2, sh.x2s, p.err, err_code(W_X2, l), D, &np[4])) fail();
+    __syncthreads();
+    TM(4);
+    __syncthreads();
+    // ---- D: the XCD's h slice ----
+    if (!dead && !gather<S::HX>(ncl, r.xl0 + XL::HH, tD, sh.hs, p.err, err_code(W_H, l), S::HX, &np[5])) fail();
+    __syncthreads();
+    TM(5);
+    __syncthreads();
+    // ---- E: x = x2 + mlp.proj(h) + b: this slot's columns from the 8 XCD partials ----
+    if (!dead && !gather_slices<D, RSC>(ncu, U::PX, r.slot, tE, sh.rsv, p.err, err_code(W_PX, l), &np[6])) fail();
+    TM(8);
+    wave_lds_sync();
+    if (!dead && lane < RSC) {
+      float sum = 0.f;
 #pragma unroll
-      for (int i = 0; i < HALF; i++) rq[i] = ld4(lo, off + i * 1024);
-#pragma unroll
-      for (int i = 0; i < HALF; i++) rq[HALF + i] = ld4(hi, off + i * 1024);
-    };
-    static_assert(S::QCW % 2 == 0, "qkv chunks split in halves");
-    // attn.proj chunks are ordered [head piece j][wave][group]: pieces past the
-    // XCD's head count lie outside the resource and read as zeros
-    auto load_p = [&](int l, bool real) {
-      const float* t = tile(l) + (size_t)NB * S::QT + (size_t)vb * S::PT;
-      const __amdgpu_buffer_rsrc_t rs = make_rsrc(t, real ? nh * NDW * G * 1024 : 0);
-#pragma unroll
-      for (int j = 0; j < S::PJ; j++)
-#pragma unroll
-        for (int g = 0; g < G; g++) rp[j * G + g] = ld4(rs, ((j * NDW + w) * G + g) * 1024 + lane * 16);
-    };
-    auto load_f = [&](int l) {
-      const float* t = tile(l) + (size_t)NB * (S::QT + S::PT) + (size_t)vb * S::FT + (size_t)w * S::FCW * D;
-      load_chunks(rf, t, true);
-    };
-    auto load_m = [&](int l) {
-      const float* t = tile(l) + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)vb * S::MT +
-                       (size_t)w * G * S::MJ * 256;
-      load_chunks(rm, t, true);
-    };
-    // cached K/V rows of this wave's keys in layer l, through buffer resources
-    // bounded by the head's ctx rows (rows at or past the new one are masked
-    // below; nothing is fetched when real == false)
-    auto load_kv = [&](int l, bool real) {
-      const size_t hoff = ((size_t)l * H + ah) * ctx * 64;
-      const int bytes = real ? ctx * 256 : 0;
-      const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + (real ? hoff : 0), bytes);
-      const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + (real ? hoff : 0), bytes);
-      const int off = key0 * 256 + lane * 16;
-#pragma unroll
-      for (int i = 0; i < KPW / 4; i++) kr[i] = ld4(rk, off + 1024 * i);
-#pragma unroll
-      for (int i = 0; i < KPW / 4; i++) vr[i] = ld4(rv, off + 1024 * i);
-    };
-#define TD(i) \
-  if (l == 1) trace_mark_d(p.trace, (i))
-    load_ln(p.vecs + S::V_LN1W, p.vecs + S::V_LN1B);
-    load_q(0, true);
-    load_p(0, true);
-    load_kv(0, wave_keys);
+      for (int x = 0; x < NX; x++) sum += sh.rsv[x * RSC + lane];
+      const int col = r.slot * RSC + lane;
+      put_pair(r.xl + XL::X + col, (sum + sh.bias_s[l & 1][S::B_M + lane]) + sh.x2s[col], tE2);
+    }
+    TM(6);
+    if (l == 1 && p.trace && lane == 0) {
+      for (int i = 1; i < 5; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
+      p.trace[r.blk * TRACE_PER + 14] = tfirst;
+      p.trace[r.blk * TRACE_PER + 15] = tvis;
+      p.trace[r.blk * TRACE_PER + 13] = tdone;
+    }
+  }
+#undef TM
+}
 
-    for (int l = 0; l < p.L; l++) {
-      const unsigned tb = tagbase + PH * l;
-      const unsigned tA = tb, tC = tb + 3, tD = tb + 5, tE = tb + 6;
-      const bool more = l + 1 < p.L;
-      const float* vl = p.vecs + (size_t)l * S::VL;
-      const float* vn = p.vecs + (size_t)(l + 1) * S::VL;  // next layer's (or ln_f after the last)
-      // ---- A: LN1 + QKV ----
-      SYNC_OK();
+// Data waves: weight tiles in registers.  Each tile is requested right after
+// the phase that consumed it, so it has a whole layer to arrive and a block
+// issues about one tile per phase (in-flight loads delay every hand-off read
+// of the CU, so they are spread evenly):
+//   A: rq(l+1)   B (attention blocks): K/V(l+1)   C: rp(l+1)   D: rf(l+1)   E: rm(l+1)
+// Every load is unconditional (an empty buffer resource past the last layer),
+// so each register has one producer and one consumer per iteration.  After a
+// failed wait (sh.fail, read after each barrier) the stores are skipped.
+#ifndef FH_FEARLY_ALL
+#define FH_FEARLY_ALL 0
+#endif
+#ifndef FH_MEARLY_ALL
+#define FH_MEARLY_ALL 0
+#endif
+#ifndef FH_FEARLY_NON
+#define FH_FEARLY_NON 1
+#endif
+#ifndef FH_MEARLY_NON
+#define FH_MEARLY_NON 1
+#endif
+template <int D, int H, bool ATTN>
+__device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const Role& r) {
+  using S = Shape<D, H>;
+  using U = Xu<D>;
+  using XL = Xl<D, H>;
+  constexpr int KC = S::KC, G = S::G;
+  // FEARLY / MEARLY: mlp.fc / mlp.proj tiles of layer l are requested right
+  // after A(l) instead of after their use in the previous layer
+  constexpr bool FEARLY = FH_FEARLY_ALL || (!ATTN && FH_FEARLY_NON);
+  constexpr bool MEARLY = FH_MEARLY_ALL || (!ATTN && FH_MEARLY_NON);
+  const int w = r.w, lane = r.lane;
+  float4 rq[S::QCW * KC], rp[S::PJ * G], rf[S::FCW * KC], rm[G * S::MJ];
+  // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
+  // lane l the dims 4*(l % 16) .. +3 of row key0 + 4i + l / 16 (one 1 KB load each)
+  constexpr int NKV = ATTN ? KPW / 4 : 1;
+  float4 kr[NKV], vr[NKV];
+  auto tile = [&](int l) { return p.tiles + (size_t)l * S::LAYER; };
+  // qkv: a block with qcw < QCW columns per wave reads its chunks twice (same
+  // addresses, no extra HBM bytes) so the loads stay unconditional
+  auto load_q = [&](int l, bool real) {
+    constexpr int HALF = S::QCW * KC / 2;
+    const float* t = tile(l) + (size_t)r.vb * S::QT + (size_t)w * r.qcw * D;
+    const __amdgpu_buffer_rsrc_t lo = make_rsrc(t, real ? HALF * 1024 : 0);
+    const __amdgpu_buffer_rsrc_t hi = make_rsrc(r.qcw == S::QCW ? t + HALF * 256 : t, real ? HALF * 1024 : 0);
+    const int off = lane * 16;
+#pragma unroll
+    for (int i = 0; i < HALF; i++) rq[i] = ld4(lo, off + i * 1024);
+#pragma unroll
+    for (int i = 0; i < HALF; i++) rq[HALF + i] = ld4(hi, off + i * 1024);
+  };
+  static_assert(S::QCW % 2 == 0, "qkv chunks split in halves");
+  // attn.proj chunks are ordered [head piece j][wave][group]: pieces past the
+  // XCD's head count lie outside the resource and read as zeros
+  auto load_p = [&](int l, bool real) {
+    const float* t = tile(l) + (size_t)NB * S::QT + (size_t)r.vb * S::PT;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(t, real ? r.nh * NDW * G * 1024 : 0);
+#pragma unroll
+    for (int j = 0; j < S::PJ; j++)
+#pragma unroll
+      for (int g = 0; g < G; g++) rp[j * G + g] = ld4(rs, ((j * NDW + w) * G + g) * 1024 + lane * 16);
+  };
+  auto load_f = [&](int l, bool real) {
+    load_chunks(rf, tile(l) + (size_t)NB * (S::QT + S::PT) + (size_t)r.vb * S::FT + (size_t)w * S::FCW * D, real);
+  };
+  auto load_m = [&](int l, bool real) {
+    load_chunks(rm,
+                tile(l) + (size_t)NB * (S::QT + S::PT + S::FT) + (size_t)r.vb * S::MT + (size_t)w * G * S::MJ * 256,
+                real);
+  };
+  // cached K/V rows of this wave's keys in layer l, through buffer resources
+  // bounded by the head's ctx rows (rows at or past the new one are masked
+  // below; nothing is fetched when real == false)
+  auto load_kv = [&](int l, bool real) {
+    const size_t hoff = ((size_t)l * H + r.ah) * p.ctx * 64;
+    const int bytes = real ? p.ctx * 256 : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.kc + (real ? hoff : 0), bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + (real ? hoff : 0), bytes);
+    const int off = r.key0 * 256 + lane * 16;
+#pragma unroll
+    for (int i = 0; i < NKV; i++) kr[i] = ld4(rk, off + 1024 * i);
+#pragma unroll
+    for (int i = 0; i < NKV; i++) vr[i] = ld4(rv, off + 1024 * i);
+  };
+#define TD(i) \
+  if (l == 1) trace_mark_d(p.trace, sh.trd, (i))
+#define DSYNC()    \
+  __syncthreads(); \
+  dead = sh.fail != 0
+  bool dead = false;
+  // Iteration l = -1 only requests layer 0's tiles, through the same load
+  // statements as every later layer: each tile register has a single load
+  // site, so no copy of an in-flight register (and no wait for it) is needed.
+  for (int l = -1; l < p.L; l++) {
+    const bool run = l >= 0;
+    const unsigned tb = r.tagbase + PH * l;
+    const unsigned tA = tb, tC = tb + 3, tD = tb + 5, tE = tb + 6;
+    const bool more = l + 1 < p.L;
+    const int ln = more ? l + 1 : l;
+    // ---- A: LN1 + QKV ----
+    if (run) {
+      DSYNC();
       TD(0);
-      // Bulk prefetches share this CU's memory queue with the control wave's
-      // polls and block the issuing wave while the queue drains.  Blocks
-      // without attention work issue almost all of theirs right after A,
-      // while the attention blocks keep the chip's critical path; attention
-      // blocks spread theirs over the phases.
-      if (attn_blk) load_f(l);
       {
-        float4 xn[KC];
-        ln_lane<KC, D>(xres, lnw, lnb, xn);
-        if (attn_blk) load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
+        float4 d[KC];
+        const float rs = ln_center<KC, D>(sh.xres, d);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::QCW; t++) {
-          if (t < qcw) {
+          if (t < r.qcw) {
             float acc = 0.f;
 #pragma unroll
-            for (int c = 0; c < KC; c++) acc += dot4(rq[t * KC + c], xn[c]);
+            for (int c = 0; c < KC; c++) acc += dot4(rq[t * KC + c], d[c]);
             const float v = wave_sum_dpp(acc);
             if (lane == t) val = v;
           }
         }
-        if (lane < qcw) {
-          const int i = slot * qc + w * qcw + lane;  // index in the XCD's column list
-          const float s = val + bias_s[l & 1][S::B_Q + w * qcw + lane];
-          put_pair(xl + XL::QKV + i, s, tA);
-          const int j = i / 192, r = i % 192, part = r / 64, e = r % 64;
+        if (!dead && lane < r.qcw) {
+          const int i = r.slot * r.qc + w * r.qcw + lane;  // index in the XCD's column list
+          const float s = val * rs + sh.bias_s[l & 1][S::B_Q + w * r.qcw + lane];
+          put_pair(r.xl + XL::QKV + i, s, tA);
+          const int j = i / 192, rr = i % 192, part = rr / 64, e = rr % 64;
           if (part > 0) {  // new K or V row of this position, for later steps
-            const int h = xcd + NX * j;
-            (part == 2 ? p.vc : p.kc)[(((size_t)l * H + h) * ctx + pos) * 64 + e] = s;
+            const int h = r.xcd + NX * j;
+            (part == 2 ? p.vc : p.kc)[(((size_t)l * H + h) * p.ctx + r.pos) * 64 + e] = s;
           }
         }
         TD(1);
-        if (!attn_blk) {
-          load_f(l);
-          load_ln(vl + S::V_LN2W, vl + S::V_LN2B);
-          load_m(l);
-          load_q(more ? l + 1 : l, more);
-        }
       }
-      // ---- B: attention of head ah over key block kb ----
-      if (attn_blk) {
-        SYNC_OK();
+      __syncthreads();  // every put of the phase is issued before any tile load
+    }
+    // early tiles of this layer (l = -1: nothing), then the next layer's qkv
+    if constexpr (FEARLY) {
+      load_f(run ? l : 0, run);
+      reload_fence();  // keeps the issue order of the tiles (the first iteration has no barriers)
+    }
+    if constexpr (MEARLY) {
+      load_m(run ? l : 0, run);
+      reload_fence();
+    }
+    // attention blocks request the next qkv tile once their own q/k/v have
+    // arrived (a queue of tile loads would delay that hand-off)
+    if constexpr (!ATTN) {
+      load_q(ln, more);
+      reload_fence();
+      if (l == 1 && p.trace) {  // trace: when this wave's requested tiles have landed
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        TD(10);
+      }
+    }
+    // ---- B: attention of head ah over key block kb ----
+    if constexpr (ATTN) {
+      if (run) {
+        DSYNC();
         TD(2);
-        load_m(l);
-        if (wave_keys) {
+      }
+      load_q(ln, more);
+      reload_fence();
+      if (run) {
+        if (r.wave_keys) {
           // lane l: dims 4*(l % 16) .. +3 of keys key0 + 4i + l / 16, i < KPW / 4
           const int g = lane >> 4, d4 = 4 * (lane & 15);
-          const float4 q4 = *reinterpret_cast<const float4*>(qkvs + d4);
-          const float4 knew = *reinterpret_cast<const float4*>(qkvs + 64 + d4);
-          const float4 vnew = *reinterpret_cast<const float4*>(qkvs + 128 + d4);
-          float sc[KPW / 4];
+          const float4 q4 = *reinterpret_cast<const float4*>(sh.qkvs + d4);
+          const float4 knew = *reinterpret_cast<const float4*>(sh.qkvs + 64 + d4);
+          const float4 vnew = *reinterpret_cast<const float4*>(sh.qkvs + 128 + d4);
+          float sc[NKV];
           float mloc = -INFINITY;
           if (l == 1 && p.trace) {  // trace: wait for the K/V rows before timing the scores
-            float z = kr[0].x + vr[KPW / 4 - 1].w;
+            float z = kr[0].x + vr[NKV - 1].w;
             asm volatile("" : "+v"(z));
             if (z == 1234.5f) mloc = 0.f;
             TD(11);
           }
 #pragma unroll
-          for (int i = 0; i < KPW / 4; i++) {
-            const int j = key0 + 4 * i + g;
-            float sp = dot4(q4, j == pos ? knew : kr[i]);
+          for (int i = 0; i < NKV; i++) {
+            const int j = r.key0 + 4 * i + g;
+            float sp = dot4(q4, j == r.pos ? knew : kr[i]);
             sp = row16_sum(sp);  // all 16 lanes of the row now hold key j's q.k
-            sc[i] = j < nk ? sp * 0.125f : -INFINITY;
+            sc[i] = j < r.nk ? sp * 0.125f : -INFINITY;
             mloc = fmaxf(mloc, sc[i]);
           }
           const float mw = wave_max_dpp(mloc);
@@ -727,12 +820,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
           float lloc = 0.f;
           float4 o4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-          for (int i = 0; i < KPW / 4; i++) {
-            const int j = key0 + 4 * i + g;
-            const float pj = j < nk ? expf(sc[i] - mw) : 0.f;
+          for (int i = 0; i < NKV; i++) {
+            const int j = r.key0 + 4 * i + g;
+            const float pj = j < r.nk ? expf(sc[i] - mw) : 0.f;
             lloc += pj;
             // rows past the new one may hold anything (even NaN): never multiplied
-            const float4 v = j < pos ? vr[i] : (j == pos ? vnew : make_float4(0.f, 0.f, 0.f, 0.f));
+            const float4 v = j < r.pos ? vr[i] : (j == r.pos ? vnew : make_float4(0.f, 0.f, 0.f, 0.f));
             o4.x += pj * v.x;
             o4.y += pj * v.y;
             o4.z += pj * v.z;
@@ -748,149 +841,293 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
             o4.w += __shfl_xor(o4.w, m, 64);
           }
           if (lane == 0) {
-            wm[w] = mw;
-            wl[w] = lw;
+            sh.wm[w] = mw;
+            sh.wl[w] = lw;
           }
-          if (g == 0) *reinterpret_cast<float4*>(&wo[w][d4]) = o4;
+          if (g == 0) *reinterpret_cast<float4*>(&sh.wo[w][d4]) = o4;
         } else {
           if (lane == 0) {
-            wm[w] = -INFINITY;
-            wl[w] = 0.f;
+            sh.wm[w] = -INFINITY;
+            sh.wl[w] = 0.f;
           }
-          wo[w][lane] = 0.f;
+          sh.wo[w][lane] = 0.f;
         }
         TD(3);
-        __syncthreads();
       }
-      // ---- C: this XCD's part of attn.proj over its heads' o ----
-      SYNC_OK();
+      if (run) {
+        __syncthreads();  // wm / wl / wo are complete
+        __syncthreads();  // the control wave has published the block's partial
+      }
+      load_kv(ln, more && r.wave_keys);
+      reload_fence();
+    }
+    // ---- C: this XCD's part of attn.proj over its heads' o ----
+    if (run) {
+      DSYNC();
       TD(4);
-      if (attn_blk) load_q(more ? l + 1 : l, more);
       {
-        const int d4 = 4 * (lane & 15), r = lane >> 4;
+        const int d4 = 4 * (lane & 15), rr = lane >> 4;
 #pragma unroll
         for (int g = 0; g < G; g++) {
           float acc = 0.f;
 #pragma unroll
           for (int j = 0; j < S::PJ; j++) {
-            const float d = dot4(rp[j * G + g], *reinterpret_cast<const float4*>(os + j * 64 + d4));
-            acc += j < nh ? d : 0.f;  // o of a missing head is stale LDS
+            const float d = dot4(rp[j * G + g], *reinterpret_cast<const float4*>(sh.os + j * 64 + d4));
+            acc += j < r.nh ? d : 0.f;  // o of a missing head is stale LDS
           }
           acc = row16_sum(acc);
-          if ((lane & 15) == 0) put_pair(p.uc + U::PX2 + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tC);
+          if (!dead && (lane & 15) == 0)
+            put_pair(p.uc + U::PX2 + r.xcd * D + r.slot * S::RSC + w * 4 * G + 4 * g + rr, acc, tC);
         }
         TD(5);
-        if (!attn_blk) {
-          load_p(more ? l + 1 : l, more);
-          load_kv(l, false);  // nothing to fetch; keeps kr / vr written on every path
-        }
       }
-      // ---- D: LN2 + mlp.fc + GELU -> this XCD's h slice ----
-      SYNC_OK();
+      __syncthreads();  // every put of the phase is issued before any tile load
+    }
+    load_p(ln, more);
+    reload_fence();
+    // ---- D: LN2 + mlp.fc + GELU -> this XCD's h slice ----
+    if (run) {
+      DSYNC();
       TD(6);
       {
-        float4 xn[KC];
-        ln_lane<KC, D>(x2s, lnw, lnb, xn);
-        load_ln(vn + S::V_LN1W, vn + S::V_LN1B);  // next layer's LN1, or LN_f after the last
+        float4 d[KC];
+        const float rs = ln_center<KC, D>(sh.x2s, d);
         float val = 0.f;
 #pragma unroll
         for (int t = 0; t < S::FCW; t++) {
           float acc = 0.f;
 #pragma unroll
-          for (int c = 0; c < KC; c++) acc += dot4(rf[t * KC + c], xn[c]);
+          for (int c = 0; c < KC; c++) acc += dot4(rf[t * KC + c], d[c]);
           const float v = wave_sum_dpp(acc);
           if (lane == t) val = v;
         }
-        if (lane < S::FCW) {
+        if (!dead && lane < S::FCW) {
           const int c = w * S::FCW + lane;
-          put_pair(xl + XL::HH + slot * S::FCOL + c, gelu_tanh(val + bias_s[l & 1][S::B_F + c]), tD);
+          put_pair(r.xl + XL::HH + r.slot * S::FCOL + c, gelu_tanh(val * rs + sh.bias_s[l & 1][S::B_F + c]), tD);
         }
         TD(7);
       }
-      // ---- E: this XCD's part of mlp.proj over its h slice ----
-      SYNC_OK();
+      __syncthreads();  // every put of the phase is issued before any tile load
+    }
+    if constexpr (!FEARLY) {
+      load_f(ln, more);
+      reload_fence();
+    }
+    // ---- E: this XCD's part of mlp.proj over its h slice ----
+    if (run) {
+      DSYNC();
       TD(8);
-      if (attn_blk) {
-        load_p(more ? l + 1 : l, more);
-        load_kv(more ? l + 1 : l, more && wave_keys);
-      }
       {
-        const int d4 = 4 * (lane & 15), r = lane >> 4;
+        const int d4 = 4 * (lane & 15), rr = lane >> 4;
 #pragma unroll
         for (int g = 0; g < G; g++) {
           float acc = 0.f;
 #pragma unroll
           for (int j = 0; j < S::MJ; j++)
-            acc += dot4(rm[g * S::MJ + j], *reinterpret_cast<const float4*>(hs + j * 64 + d4));
+            acc += dot4(rm[g * S::MJ + j], *reinterpret_cast<const float4*>(sh.hs + j * 64 + d4));
           acc = row16_sum(acc);
-          if ((lane & 15) == 0) put_pair(p.uc + U::PX + xcd * D + slot * RSC + w * 4 * G + 4 * g + r, acc, tE);
+          if (!dead && (lane & 15) == 0)
+            put_pair(p.uc + U::PX + r.xcd * D + r.slot * S::RSC + w * 4 * G + 4 * g + rr, acc, tE);
         }
         TD(9);
       }
+      __syncthreads();  // every put of the phase is issued before any tile load
     }
+    if constexpr (!MEARLY) {
+      load_m(ln, more);
+      reload_fence();
+    }
+  }
 #undef TD
-    if (ok) {
-      // ---- head: LN_f + tied projection over this block's vocab rows ----
-      const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
-      constexpr int HG = 4;    // rows per wave in flight
-      const float* E = p.tok + (size_t)blk * R * D;
-      float4 rh[HG * KC];
-      const int nrow = (R - w + NDW - 1) / NDW;  // rows of this wave
+#undef DSYNC
+}
+
+template <int D, int H>
+__global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
+  using S = Shape<D, H>;
+  using XL = Xl<D, H>;
+  constexpr int KC = S::KC;
+  __shared__ Lds<D, H> sh;
+
+  Role r;
+  const int tid = threadIdx.x;
+  r.blk = blockIdx.x;
+  // w is wave-uniform; readfirstlane lets the compiler know, so buffer
+  // resources built from it stay in scalar registers
+  r.w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  r.lane = tid & 63;
+  const bool ctrl = r.w == NW - 1;
+  // The dispatcher deals consecutive blocks to consecutive XCDs, continuing
+  // from wherever the previous dispatch stopped: the XCD comes from the
+  // hardware, and blocks b = 8k .. 8k+7 (slot k) land on 8 different XCDs.
+  r.xcd = (int)xcc_id() & (NX - 1);
+  r.slot = r.blk / NX;
+  // every tile and bias depends on (XCD, slot): they are stored under the
+  // virtual block id vb; the head rows are indexed by blk
+  r.vb = r.slot * NX + r.xcd;
+  if (tid == 0) sh.fail = 0;
+  if (tid < 16) sh.trd[tid] = tid == 13 ? (unsigned long long)(xcc_id() & (NX - 1)) : 0ull;
+  r.tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
+  trace_mark(p.trace, 30);
+
+  const int n = *p.src.step;
+  r.pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token (>= 1)
+  int tokid = p.src.tokens[p.src.tok_off + n];
+  if ((unsigned)tokid >= (unsigned)p.V) tokid = 0;
+  r.xl = p.xl + (size_t)r.xcd * XL::STRIDE;
+  r.xl0 = r.xcd * XL::STRIDE;
+  // qkv columns: the XCD's heads h = xcd + 8j (j < nh) own columns
+  // [j*192, j*192+192) of the XCD's list (q, k, v of each head); slot s has qc of them
+  r.nh = (H - r.xcd + NX - 1) / NX;
+  r.qc = 3 * S::HD * r.nh / SLOTS;
+  r.qcw = r.qc / NDW;
+  // attention role: local head hj = slot / SPH, key block kb = slot % SPH
+  r.hj = r.slot / S::SPH;
+  r.kb = r.slot % S::SPH;
+  r.ah = r.xcd + NX * r.hj;
+  r.nk = r.pos + 1;
+  r.nkb = (r.nk + KPB - 1) / KPB;
+  const bool attn_blk = r.hj < r.nh && r.kb < r.nkb;
+  r.key0 = r.kb * KPB + r.w * KPW;
+  r.wave_keys = attn_blk && r.key0 < r.nk;
+
+  // x = tok_emb[id] + pos_emb[pos] (every block keeps its own copy)
+  for (int i = tid; i < D; i += NT) sh.xres[i] = p.tok[(size_t)tokid * D + i] + p.pos[(size_t)r.pos * D + i];
+
+  // The control wave and the data waves run separate loops, specialised by
+  // the block's role, that meet at the same sequence of barriers; a failed
+  // wait makes every wave leave at the next barrier.
+  if (ctrl) {
+    if (attn_blk)
+      ctrl_loop<D, H, true>(p, sh, r);
+    else
+      ctrl_loop<D, H, false>(p, sh, r);
+  } else {
+    if (attn_blk)
+      data_loop<D, H, true>(p, sh, r);
+    else
+      data_loop<D, H, false>(p, sh, r);
+  }
+  const int lane = r.lane, w = r.w;
+  const unsigned tH = r.tagbase + PH * p.L;
+  if (ctrl) {
+    // ---- head: the final x ----
+    const NcBuf ncu(p.uc, p.uc_bytes);
+    const LcBuf ncl(p.xl, p.xl_bytes);
+    if (!sh.fail &&
+        !gather<D>(ncl, r.xl0 + XL::X, r.tagbase + PH * (p.L - 1) + 7, sh.xres, p.err, err_code(W_XF, 0)))
+      sh.fail = 1;
+    __syncthreads();
+    if (!sh.fail) {
+      __syncthreads();  // hval holds this block's logits
+      // block 0 collects every block's argmax: it proves all blocks read this
+      // launch's counter, so the counter can advance
+      if (r.blk == 0) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        long it = 0;
+        bool good = true;
+        for (;;) {
+          reload_fence();
+          bool okk = true;
+          best = -INFINITY;
+          bi = 0x7fffffff;
 #pragma unroll
-      for (int t = 0; t < HG; t++) {
-        const int row = w + NDW * min(t, nrow - 1);
+          for (int i = 0; i < NB / 64; i++) {
+            const uint4 a = ncu.load4(p.off_amax + 16 * (i * 64 + lane));
+            okk &= a.z == tH;
+            argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
+          }
+          if (__all(okk)) break;
+          if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+            if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_AMAX, 0));
+            good = false;
+            break;
+          }
+        }
+        if (good) {
+          wave_argmax(best, bi);
+          if (lane == 0) {
+            if (p.greedy) {
+              const int total = p.src.tok_off + 1 + n;  // prompt_len + n
+              p.tokens_out[total] = bi;
+              if (n < p.max_new) p.out_ids[n] = bi;
+              if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+              *p.step_out = n + 1;
+            }
+            __hip_atomic_fetch_add(p.launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+    }
+  } else {
+    // ---- head: LN_f + tied projection over this block's vocab rows ----
+    const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
+    constexpr int HG = 4;    // rows per wave in flight
+    const float* E = p.tok + (size_t)r.blk * R * D;
+    float4 lnw[KC], lnb[KC];
+    {
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.vecs, D * 4), rb = make_rsrc(p.vecs + D, D * 4);
 #pragma unroll
-        for (int c = 0; c < KC; c++)
-          rh[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+      for (int c = 0; c < KC; c++) {
+        lnw[c] = ld4(rw, c * 1024 + lane * 16);
+        lnb[c] = ld4(rb, c * 1024 + lane * 16);
+      }
+    }
+    float4 rh[HG * KC];
+    const int nrow = (R - w + NDW - 1) / NDW;  // rows of this wave
+#pragma unroll
+    for (int t = 0; t < HG; t++) {
+      const int row = w + NDW * min(t, nrow - 1);
+#pragma unroll
+      for (int c = 0; c < KC; c++)
+        rh[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+    }
+    __syncthreads();
+    if (!sh.fail) {
+      float4 xn[KC];
+      ln_lane<KC, D>(sh.xres, lnw, lnb, xn);
+      for (int g = 0; g < nrow; g += HG) {
+        float4 nx[HG * KC];
+#pragma unroll
+        for (int t = 0; t < HG; t++) {
+          const int row = w + NDW * min(g + HG + t, nrow - 1);
+#pragma unroll
+          for (int c = 0; c < KC; c++)
+            nx[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+        }
+#pragma unroll
+        for (int t = 0; t < HG; t++) {
+          if (g + t < nrow) {
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < KC; c++) acc += dot4(rh[t * KC + c], xn[c]);
+            const float v = wave_sum_dpp(acc);
+            if (lane == 0) sh.hval[w + NDW * (g + t)] = v;
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
       }
       __syncthreads();
-      ok = !fail_s;
-      if (ok) {
-        float4 xn[KC];
-        ln_lane<KC, D>(xres, lnw, lnb, xn);
-        for (int g = 0; g < nrow; g += HG) {
-          float4 nx[HG * KC];
-#pragma unroll
-          for (int t = 0; t < HG; t++) {
-            const int row = w + NDW * min(g + HG + t, nrow - 1);
-#pragma unroll
-            for (int c = 0; c < KC; c++)
-              nx[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
-          }
-#pragma unroll
-          for (int t = 0; t < HG; t++) {
-            if (g + t < nrow) {
-              float acc = 0.f;
-#pragma unroll
-              for (int c = 0; c < KC; c++) acc += dot4(rh[t * KC + c], xn[c]);
-              const float v = wave_sum_dpp(acc);
-              if (lane == 0) hval[w + NDW * (g + t)] = v;
-            }
-          }
-#pragma unroll
-          for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
+      if (w == 0) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        if (lane < R) {
+          const float s = sh.hval[lane];
+          const int v = r.blk * R + lane;
+          p.logits[v] = s;
+          best = s;
+          bi = v;
         }
-        __syncthreads();
-        if (w == 0) {
-          const unsigned tH = tagbase + PH * p.L;
-          float best = -INFINITY;
-          int bi = 0x7fffffff;
-          if (lane < R) {
-            const float s = hval[lane];
-            const int v = blk * R + lane;
-            p.logits[v] = s;
-            best = s;
-            bi = v;
-          }
-          wave_argmax(best, bi);
-          if (lane == 0)
-            *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * blk) =
-                make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
-        }
+        wave_argmax(best, bi);
+        if (lane == 0)
+          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
+              make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
       }
     }
   }
-#undef SYNC_OK
+  if (ctrl && p.trace && lane < 14) p.trace[r.blk * TRACE_PER + 16 + lane] = sh.trd[lane];
   trace_mark(p.trace, 31);
 }
 
@@ -898,15 +1135,27 @@ __global__ void k_xcc_probe(unsigned* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
 
-// tile[b][c][k] = W[k][map[b*ncol + c]] (0 where map < 0), W row-major [K][N]
+// tile[b][c][k] = scale[k] * W[k][map[b*ncol + c]] (0 where map < 0), W row-major
+// [K][N]: the LayerNorm weight in front of the matrix folded into its rows
 __global__ void k_relayout(const float* __restrict__ W, int K, int N, const int* __restrict__ map, int ncol,
-                           float* __restrict__ tile) {
+                           const float* __restrict__ scale, float* __restrict__ tile) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= (size_t)NB * ncol * K) return;
   const int k = (int)(i % K);
   const size_t bc = i / K;
   const int col = map[bc];
-  tile[i] = col >= 0 ? W[(size_t)k * N + col] : 0.f;
+  tile[i] = col >= 0 ? scale[k] * W[(size_t)k * N + col] : 0.f;
+}
+
+// out[n] = bias[n] + sum_k shift[k] * W[k][n]: the LayerNorm bias in front of
+// the matrix folded into the matrix's bias (accumulated in double)
+__global__ void k_fold_bias(const float* __restrict__ W, int K, int N, const float* __restrict__ shift,
+                            const float* __restrict__ bias, float* __restrict__ out) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= N) return;
+  double s = 0.0;
+  for (int k = 0; k < K; k++) s += (double)shift[k] * (double)W[(size_t)k * N + n];
+  out[n] = (float)((double)bias[n] + s);
 }
 
 // chunks of 4 columns x 64 rows: tile[ch*256 + 4l + q] = W[k0 + 4*(l%16) + q][c0 + l/16]
@@ -1046,8 +1295,7 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   }
   tile_floats = S768::LAYER * L;
   if (hipMalloc(&tiles, tile_floats * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
-  const size_t vec_floats = (size_t)S768::VL * L + 2 * D;
-  if (hipMalloc(&vecs, vec_floats * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
+  if (hipMalloc(&vecs, 2 * (size_t)D * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
   if (hipMalloc(&btab, (size_t)L * NB * S768::BT * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
   xch_bytes = uc_total_bytes(D);
   uc = static_cast<char*>(uc_take(device, xch_bytes));
@@ -1074,20 +1322,26 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
   char* dmap = nullptr;
   const size_t nq = m.q.size() * 4, nf = m.f.size() * 4, nr = m.rs.size() * 4, np = m.pc.size() * 8,
                nmc = m.mc.size() * 8;
-  if (hipMalloc(&dmap, nq + nf + nr + np + nmc) != hipSuccess) return FH_ERR_OOM;
+  if (hipMalloc(&dmap, nq + nf + nr + np + nmc + 7 * (size_t)D * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
   int* dq = reinterpret_cast<int*>(dmap);
   int* df = reinterpret_cast<int*>(dmap + nq);
   int* dr = reinterpret_cast<int*>(dmap + nq + nf);
   int2* dp = reinterpret_cast<int2*>(dmap + nq + nf + nr);
   int2* dm = reinterpret_cast<int2*>(dmap + nq + nf + nr + np);
+  float* fold = reinterpret_cast<float*>(dmap + nq + nf + nr + np + nmc);  // folded qkv (3D) and fc (4D) biases
   int rc = FH_OK;
   auto copy = [&](const float* src, float* dst, int n) {
     hipLaunchKernelGGL(k_copy, dim3((n + 255) / 256), dim3(256), 0, st, src, dst, n);
     return hipGetLastError() == hipSuccess;
   };
-  auto relayout = [&](const float* W, int K, int N, const int* map, int ncol, float* out) {
+  auto relayout = [&](const float* W, int K, int N, const int* map, int ncol, const float* scale, float* out) {
     const size_t tot = (size_t)NB * ncol * K;
-    hipLaunchKernelGGL(k_relayout, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, W, K, N, map, ncol, out);
+    hipLaunchKernelGGL(k_relayout, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, W, K, N, map, ncol, scale,
+                       out);
+    return hipGetLastError() == hipSuccess;
+  };
+  auto fold_bias = [&](const float* W, int K, int N, const float* shift, const float* b, float* out) {
+    hipLaunchKernelGGL(k_fold_bias, dim3((N + 255) / 256), dim3(256), 0, st, W, K, N, shift, b, out);
     return hipGetLastError() == hipSuccess;
   };
   auto chunks = [&](const float* W, int N, const int2* desc, int nch, float* out) {
@@ -1112,20 +1366,19 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
     const float* const* PL = params + 2 + 12 * l;
     float* bt = btab + (size_t)l * NB * S::BT;
     // registry slots: 0 ln1.w 1 ln1.b 2 qkv.w 3 qkv.b 4 proj.w 5 proj.b 6 ln2.w 7 ln2.b 8 fc.w 9 fc.b 10 mproj.w 11 mproj.b
-    const bool good = relayout(PL[2], D, 3 * D, dq, S::QCMAX, tl) &&
+    // LN1 is folded into qkv (weight into the rows, bias into qkv.b), LN2 into mlp.fc
+    const bool good = relayout(PL[2], D, 3 * D, dq, S::QCMAX, PL[0], tl) &&
                       chunks(PL[4], D, dp, (int)m.pc.size(), tl + (size_t)NB * S::QT) &&
-                      relayout(PL[8], D, 4 * D, df, S::FCOL, tl + (size_t)NB * (S::QT + S::PT)) &&
+                      relayout(PL[8], D, 4 * D, df, S::FCOL, PL[6], tl + (size_t)NB * (S::QT + S::PT)) &&
                       chunks(PL[10], D, dm, (int)m.mc.size(), tl + (size_t)NB * (S::QT + S::PT + S::FT)) &&
-                      bias(PL[3], dq, S::QCMAX, S::B_Q, bt) && bias(PL[9], df, S::FCOL, S::B_F, bt) &&
+                      fold_bias(PL[2], D, 3 * D, PL[1], PL[3], fold) &&
+                      fold_bias(PL[8], D, 4 * D, PL[7], PL[9], fold + 3 * D) &&
+                      bias(fold, dq, S::QCMAX, S::B_Q, bt) && bias(fold + 3 * D, df, S::FCOL, S::B_F, bt) &&
                       bias(PL[5], dr, S::RSC, S::B_P, bt) && bias(PL[11], dr, S::RSC, S::B_M, bt);
-    float* vl = vecs + (size_t)l * S::VL;
-    if (!good || !copy(PL[0], vl + S::V_LN1W, D) || !copy(PL[1], vl + S::V_LN1B, D) ||
-        !copy(PL[6], vl + S::V_LN2W, D) || !copy(PL[7], vl + S::V_LN2B, D))
-      rc = FH_ERR_HIP;
+    if (!good) rc = FH_ERR_HIP;
   }
   const float* const* PF = params + 2 + 12 * L;
-  if (rc == FH_OK && (!copy(PF[0], vecs + (size_t)S::VL * L, D) || !copy(PF[1], vecs + (size_t)S::VL * L + D, D)))
-    rc = FH_ERR_HIP;
+  if (rc == FH_OK && (!copy(PF[0], vecs, D) || !copy(PF[1], vecs + D, D))) rc = FH_ERR_HIP;
   if (hipStreamSynchronize(st) != hipSuccess) rc = FH_ERR_HIP;
   (void)hipFree(dmap);
   return rc;

@@ -17,7 +17,7 @@ struct FastDecode {
   int blocks = 0;
   int device = 0;
   float* tiles = nullptr;            // per-block weight tiles, column-major
-  float* vecs = nullptr;             // LayerNorm parameters at fixed offsets
+  float* vecs = nullptr;             // ln_f weight and bias (LN1 / LN2 are folded into the tiles)
   float* btab = nullptr;             // per-layer, per-block bias slices
   char* uc = nullptr;                // uncached hand-off area (cross-XCD pairs, argmax records)
   size_t xch_bytes = 0;
