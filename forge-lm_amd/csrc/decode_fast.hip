@@ -288,6 +288,15 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// max over the 16 lanes of each DPP row
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 __device__ __forceinline__ float dot4(const float4 a, const float4 b) {
   return a.x * b.x + a.y * b.y + a.z * b.z + a.w * b.w;
 }
@@ -344,6 +353,15 @@ __device__ __forceinline__ void load_chunks(float4 (&r)[N], const float* tile, b
   for (int i = 0; i < N; i++) r[i] = ld4(rs, off + i * 1024);
 }
 
+// GELU (tanh form, CpuBackend.Gelu) with tanh(u) = 1 - 2 / (exp(2u) + 1) on the
+// hardware exponential: within a few 1e-7 of the libm form
+__device__ __forceinline__ float gelu_fast(float v) {
+  const float C = 0.7978845238685608f;  // MathF.Sqrt(2f / MathF.PI) in fp32
+  const float u = C * (v + 0.044715f * v * v * v);
+  const float t = 1.f - 2.f * __frcp_rn(__expf(2.f * u) + 1.f);
+  return 0.5f * v * (1.f + t);
+}
+
 // LayerNorm statistics of xin[D] (LDS) for this lane's elements k = c*256 +
 // lane*4 + 0..3: d = x - mu, returns rs = 1 / sqrt(var + 1e-5) (biased
 // variance, CpuBackend.LayerNormForward).  The LayerNorm weight is folded into
@@ -368,7 +386,7 @@ __device__ __forceinline__ float ln_center(const float* xin, float4 (&d)[KC]) {
     v += (d[c].x * d[c].x + d[c].y * d[c].y) + (d[c].z * d[c].z + d[c].w * d[c].w);
   }
   const float var = wave_sum_dpp(v);
-  return 1.f / sqrtf(var / (float)D + 1e-5f);
+  return __frsqrt_rn(var / (float)D + 1e-5f);
 }
 
 // Control wave: the attention partials of the XCD's nh heads, nkb key blocks
@@ -425,31 +443,12 @@ __device__ bool gather_parts(const B& nc, int pair0, int nh, int nkb, unsigned t
                              long* npoll = nullptr, unsigned long long* tfirst = nullptr) {
   using S = Shape<D, H>;
   static_assert((S::HPX * S::SPH * PART / 2 + 63) / 64 <= 17, "partial loads per lane");
+  // a few sizes keep the code small (extra lanes re-read the last unit)
   const int ra = (nh * nkb * (PART / 2) + 63) / 64;
-#define FH_PARTS_CASE(k) \
-  case k:                \
-    return gather_parts_r<D, H, k>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
-  switch (ra) {
-    FH_PARTS_CASE(1)
-    FH_PARTS_CASE(2)
-    FH_PARTS_CASE(3)
-    FH_PARTS_CASE(4)
-    FH_PARTS_CASE(5)
-    FH_PARTS_CASE(6)
-    FH_PARTS_CASE(7)
-    FH_PARTS_CASE(8)
-    FH_PARTS_CASE(9)
-    FH_PARTS_CASE(10)
-    FH_PARTS_CASE(11)
-    FH_PARTS_CASE(12)
-    FH_PARTS_CASE(13)
-    FH_PARTS_CASE(14)
-    FH_PARTS_CASE(15)
-    FH_PARTS_CASE(16)
-    default:
-      return gather_parts_r<D, H, 17>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
-  }
-#undef FH_PARTS_CASE
+  if (ra <= 3) return gather_parts_r<D, H, 3>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
+  if (ra <= 6) return gather_parts_r<D, H, 6>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
+  if (ra <= 11) return gather_parts_r<D, H, 11>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
+  return gather_parts_r<D, H, 17>(nc, pair0, nh, nkb, tag, out, err, code, npoll, tfirst);
 }
 
 // LDS of one block
@@ -465,6 +464,7 @@ struct Lds {
   __align__(16) float wo[NW][64];                      // per-wave attention partials
   __align__(16) float parts[S::HPX * S::SPH * PART];  // attention partials of the XCD's heads
   float pw[64];                                        // their weights in the combination
+  float pl[4];                                         // and each head's softmax denominator
   float wm[NW], wl[NW];
   float bias_s[2][S::BT];
   float hval[S::RMAX];
@@ -485,13 +485,13 @@ struct Role {
   int xl0;              // same, as a pair index into p.xl
 };
 
-// Control wave: collects every hand-off.  ATTN: this block computes attention
+// Control wave: collects every hand-off.  attn: this block computes attention
 // (it gathers its head's q/k/v and publishes the block's partial).  After a
 // failed wait (sh.fail) it skips the remaining waits and stores but meets
 // every barrier: the loops have no early exit, which keeps the compiler's
 // load-wait bookkeeping exact across iterations.
-template <int D, int H, bool ATTN>
-__device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const Role& r) {
+template <int D, int H>
+__device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const Role& r, const bool attn) {
   using S = Shape<D, H>;
   using U = Xu<D>;
   using XL = Xl<D, H>;
@@ -501,7 +501,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
   const LcBuf ncl(p.xl, p.xl_bytes);
   bool dead = false;
   long np[7] = {0, 0, 0, 0, 0, 0, 0};  // polls per gather (trace)
-  unsigned long long tfirst = 0, tvis = 0, tdone = 0;
+  unsigned long long tfirst = 0, tvis = 0, tdone = 0, tcomb = 0;
   auto fail = [&]() {
     dead = true;
     sh.fail = 1;
@@ -523,7 +523,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     // behind the tile loads of another wave of this CU.
     __syncthreads();
     // ---- B: attention of this block's keys; publish the block's partial ----
-    if constexpr (ATTN) {
+    if (attn) {
       if (!dead && !gather<192>(ncl, r.xl0 + XL::QKV + r.hj * 192, tA, sh.qkvs, p.err, err_code(W_QKV, l), 192,
                                 &np[1]))
         fail();
@@ -536,7 +536,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       float Ls = 0.f, o = 0.f;
 #pragma unroll
       for (int i = 0; i < NDW; i++) {
-        const float f = (sh.wm[i] == -INFINITY) ? 0.f : expf(sh.wm[i] - M);
+        const float f = (sh.wm[i] == -INFINITY) ? 0.f : __expf(sh.wm[i] - M);
         Ls += sh.wl[i] * f;
         o += sh.wo[i][lane] * f;
       }
@@ -564,32 +564,37 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       fail();
     if (l == 1 && p.trace) tdone = wall_clock64();
     if (!dead) {
-      // lane t < nh * nkb holds partial (j, c) = (t / nkb, t % nkb): its weight
-      // exp(m - M_j) goes to sh.pw; then lane d sums o[d] over the head's partials
+      // DPP row j (lanes 16j .. 16j+15) holds head j's partials, lane 16j + c
+      // partial c: its weight exp(m - M_j) goes to sh.pw, the row sums l * weight;
+      // then lane d sums o[d] over the head's partials (reads issued together,
+      // partials past nkb masked)
+      static_assert(S::SPH == 16 && S::HPX <= 4, "one DPP row of partials per head");
       wave_lds_sync();
-      const int np = r.nh * r.nkb, jt = lane / r.nkb, ct = lane - jt * r.nkb;
-      const bool has = lane < np;
+      const int jt = lane >> 4, ct = lane & 15;
+      const bool has = jt < r.nh && ct < r.nkb;
       const float mt = has ? sh.parts[(jt * S::SPH + ct) * PART + 64] : -INFINITY;
       const float lt = has ? sh.parts[(jt * S::SPH + ct) * PART + 65] : 0.f;
-      float Lj[S::HPX];
-#pragma unroll
-      for (int j = 0; j < S::HPX; j++) {
-        const float Mj = wave_max_dpp(has && jt == j ? mt : -INFINITY);
-        const float f = (has && jt == j) ? expf(mt - Mj) : 0.f;
-        Lj[j] = wave_sum_dpp(lt * f);
-        if (has && jt == j) sh.pw[lane] = f;
-      }
+      const float Mj = row16_max(mt);
+      const float f = has ? __expf(mt - Mj) : 0.f;
+      const float Lrow = row16_sum(lt * f);
+      sh.pw[lane] = f;
+      if (ct == 0) sh.pl[jt] = Lrow;
       wave_lds_sync();
 #pragma unroll
       for (int j = 0; j < S::HPX; j++) {
         if (j < r.nh) {
           const float* pj = sh.parts + j * S::SPH * PART;
           float o = 0.f;
-          for (int c = 0; c < r.nkb; c++) o += pj[c * PART + lane] * sh.pw[j * r.nkb + c];
-          sh.os[j * 64 + lane] = o / Lj[j];
+#pragma unroll
+          for (int c = 0; c < S::SPH; c++) {
+            const float t = pj[c * PART + lane] * sh.pw[j * 16 + c];
+            o += c < r.nkb ? t : 0.f;
+          }
+          sh.os[j * 64 + lane] = o * __frcp_rn(sh.pl[j]);
         }
       }
     }
+    if (l == 1 && p.trace) tcomb = wall_clock64();
     __syncthreads();
     TM(3);
     __syncthreads();
@@ -626,9 +631,9 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     }
     TM(6);
     if (l == 1 && p.trace && lane == 0) {
-      for (int i = 1; i < 5; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
+      for (int i = 1; i < 3; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
       p.trace[r.blk * TRACE_PER + 14] = tfirst;
-      p.trace[r.blk * TRACE_PER + 15] = tvis;
+      p.trace[r.blk * TRACE_PER + 15] = tcomb;
       p.trace[r.blk * TRACE_PER + 13] = tdone;
     }
   }
@@ -822,7 +827,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
 #pragma unroll
           for (int i = 0; i < NKV; i++) {
             const int j = r.key0 + 4 * i + g;
-            const float pj = j < r.nk ? expf(sc[i] - mw) : 0.f;
+            const float pj = j < r.nk ? __expf(sc[i] - mw) : 0.f;
             lloc += pj;
             // rows past the new one may hold anything (even NaN): never multiplied
             const float4 v = j < r.pos ? vr[i] : (j == r.pos ? vnew : make_float4(0.f, 0.f, 0.f, 0.f));
@@ -863,6 +868,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
     }
     // ---- C: this XCD's part of attn.proj over its heads' o ----
     if (run) {
+      TD(13);
       DSYNC();
       TD(4);
       {
@@ -903,7 +909,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
         }
         if (!dead && lane < S::FCW) {
           const int c = w * S::FCW + lane;
-          put_pair(r.xl + XL::HH + r.slot * S::FCOL + c, gelu_tanh(val * rs + sh.bias_s[l & 1][S::B_F + c]), tD);
+          put_pair(r.xl + XL::HH + r.slot * S::FCOL + c, gelu_fast(val * rs + sh.bias_s[l & 1][S::B_F + c]), tD);
         }
         TD(7);
       }
@@ -966,7 +972,8 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // virtual block id vb; the head rows are indexed by blk
   r.vb = r.slot * NX + r.xcd;
   if (tid == 0) sh.fail = 0;
-  if (tid < 16) sh.trd[tid] = tid == 13 ? (unsigned long long)(xcc_id() & (NX - 1)) : 0ull;
+  if (tid < 16) sh.trd[tid] = 0ull;
+  if (p.trace && tid == NT - 64) p.trace[r.blk * TRACE_PER + 12] = (unsigned long long)r.xcd;
   r.tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
   trace_mark(p.trace, 30);
 
@@ -998,10 +1005,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // the block's role, that meet at the same sequence of barriers; a failed
   // wait makes every wave leave at the next barrier.
   if (ctrl) {
-    if (attn_blk)
-      ctrl_loop<D, H, true>(p, sh, r);
-    else
-      ctrl_loop<D, H, false>(p, sh, r);
+    ctrl_loop<D, H>(p, sh, r, attn_blk);
   } else {
     if (attn_blk)
       data_loop<D, H, true>(p, sh, r);
