@@ -187,6 +187,7 @@ struct KParams {
   unsigned* launch;   // launch counter
   int* err;
   int V, ctx, L, max_new, eos, greedy;
+  int nsteps;         // decode steps of this launch (greedy: the argmax feeds the next step)
   int* tokens_out;    // same buffer as src.tokens, written by the greedy argmax
   int* step_out;      // same word as src.step
   unsigned long long* trace;  // optional: block 0 timestamps
@@ -341,6 +342,13 @@ __device__ __forceinline__ float4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
   return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
 }
 
+// the same through the L2 (the SC1 policy misses the CU's L1): for rows that
+// other CUs write during the launch (the KV cache)
+__device__ __forceinline__ float4 ld4_l2(__amdgpu_buffer_rsrc_t r, int off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
 // r[i] = chunk i of a tile (chunk = 64 lanes x float4 = 1 KB).  Loads through a
 // buffer resource: one base in scalar registers and constant offsets; with
 // real == false the resource is empty and the loads return zeros without
@@ -468,6 +476,7 @@ struct Lds {
   float wm[NW], wl[NW];
   float bias_s[2][S::BT];
   float hval[S::RMAX];
+  __align__(16) float lnf[2 * D];  // ln_f weight, bias
   unsigned long long trd[16];  // data wave 0's trace marks (0..13)
   int fail;
 };
@@ -477,10 +486,12 @@ struct Role {
   int blk, w, lane, xcd, slot, vb;
   int nh, qc, qcw;      // heads of the XCD; qkv columns of the block and of a data wave
   int hj, kb, ah;       // attention: local head, key block, global head
-  int pos, nk, nkb;     // new position, keys, key blocks per head
+  int n0, pos0;         // first step of the launch and its position
+  int pos, nk;          // the current token's position and key count
+  int nkb;              // key blocks per head (attention blocks) for every token of the launch
   int key0;             // this data wave's first key
   bool wave_keys;
-  unsigned tagbase;
+  unsigned tag0;        // tag base of the launch's first token
   uint2* xl;            // this XCD's local pairs
   int xl0;              // same, as a pair index into p.xl
 };
@@ -490,6 +501,32 @@ struct Role {
 // failed wait (sh.fail) it skips the remaining waits and stores but meets
 // every barrier: the loops have no early exit, which keeps the compiler's
 // load-wait bookkeeping exact across iterations.
+// Control wave, head of a token: waits until every block's argmax record carries
+// `tag`, then returns the overall (first) maximum in best / bi.
+__device__ bool gather_argmax(const NcBuf& nc, int off, unsigned tag, float& best, int& bi, int* err, int code) {
+  const int lane = threadIdx.x & 63;
+  long it = 0;
+  for (;;) {
+    reload_fence();
+    bool ok = true;
+    best = -INFINITY;
+    bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < NB / 64; i++) {
+      const uint4 a = nc.load4(off + 16 * (i * 64 + lane));
+      ok &= a.z == tag;
+      argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
+    }
+    if (__all(ok)) break;
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
+      return false;
+    }
+  }
+  wave_argmax(best, bi);
+  return true;
+}
+
 template <int D, int H>
 __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const Role& r, const bool attn) {
   using S = Shape<D, H>;
@@ -501,15 +538,19 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
   const LcBuf ncl(p.xl, p.xl_bytes);
   bool dead = false;
   long np[7] = {0, 0, 0, 0, 0, 0, 0};  // polls per gather (trace)
-  unsigned long long tfirst = 0, tvis = 0, tdone = 0, tcomb = 0;
+  unsigned long long tfirst = 0, tdone = 0, tcomb = 0;
   auto fail = [&]() {
     dead = true;
     sh.fail = 1;
   };
 #define TM(i) \
-  if (l == 1) trace_mark(p.trace, (i))
-  for (int l = 0; l < p.L; l++) {
-    const unsigned tb = r.tagbase + PH * l;
+  if (it == 1) trace_mark(p.trace, (i))
+  // tokens t < nsteps, layers l < L: one flat loop
+  const int total = p.nsteps * p.L;
+  for (int it = 0; it < total; it++) {
+    const int t = it / p.L, l = it - t * p.L;
+    const unsigned tbase = r.tag0 + (unsigned)t * TAGS;
+    const unsigned tb = tbase + PH * l;
     const unsigned tA = tb, tP = tb + 1, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6, tE2 = tb + 7;
     // ---- A: x of this layer (every XCD's copy) ----
     for (int i = lane; i < S::BT; i += 64) sh.bias_s[l & 1][i] = p.btab[((size_t)l * NB + r.vb) * S::BT + i];
@@ -517,7 +558,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       fail();
     __syncthreads();
     TM(0);
-    if (l == 2) trace_mark(p.trace, 9);
+    if (it == 2) trace_mark(p.trace, 9);
     // Every phase whose data waves publish and then request tiles has a
     // second barrier between the two, so that no published value queues
     // behind the tile loads of another wave of this CU.
@@ -546,23 +587,14 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         if (lane < PART - 64) put_pair(pp + 64 + lane, lane == 0 ? M : (lane == 1 ? Ls : 0.f), tP);
       }
       TM(2);
-      if (l == 1 && p.trace) {  // trace: when this block's own partial reads back
-        const int pb = (r.xl0 + XL::PARTS + (r.hj * S::SPH + r.kb) * PART) * 8;
-        for (long it = 0; it < SPIN_LIMIT; it++) {
-          reload_fence();
-          const uint4 v = ncl.load4(pb + lane * 16);
-          if (__all(lane >= PART / 2 || (v.y == tP && v.w == tP))) break;
-        }
-        tvis = wall_clock64();
-      }
       __syncthreads();  // the partial is published before the data waves request K/V
     }
     // ---- C: o of the XCD's heads from every key block's partial ----
     if (!dead &&
         !gather_parts<D, H>(ncl, r.xl0 + XL::PARTS, r.nh, r.nkb, tP, sh.parts, p.err, err_code(W_PART, l), &np[2],
-                            (l == 1 && p.trace) ? &tfirst : nullptr))
+                            (it == 1 && p.trace) ? &tfirst : nullptr))
       fail();
-    if (l == 1 && p.trace) tdone = wall_clock64();
+    if (it == 1 && p.trace) tdone = wall_clock64();
     if (!dead) {
       // DPP row j (lanes 16j .. 16j+15) holds head j's partials, lane 16j + c
       // partial c: its weight exp(m - M_j) goes to sh.pw, the row sums l * weight;
@@ -594,7 +626,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         }
       }
     }
-    if (l == 1 && p.trace) tcomb = wall_clock64();
+    if (it == 1 && p.trace) tcomb = wall_clock64();
     __syncthreads();
     TM(3);
     __syncthreads();
@@ -630,14 +662,55 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       put_pair(r.xl + XL::X + col, (sum + sh.bias_s[l & 1][S::B_M + lane]) + sh.x2s[col], tE2);
     }
     TM(6);
-    if (l == 1 && p.trace && lane == 0) {
+    if (it == 1 && p.trace && lane == 0) {
       for (int i = 1; i < 3; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
       p.trace[r.blk * TRACE_PER + 14] = tfirst;
       p.trace[r.blk * TRACE_PER + 15] = tcomb;
       p.trace[r.blk * TRACE_PER + 13] = tdone;
     }
+    if (l == p.L - 1) {
+      // ---- head of token t: the final x, this block's logits, every block's argmax ----
+      if (!dead && !gather<D>(ncl, r.xl0 + XL::X, tb + 7, sh.xres, p.err, err_code(W_XF, 0))) fail();
+      __syncthreads();  // x is in xres: the data waves compute this block's logits
+      __syncthreads();  // data wave 0 publishes the block's argmax record
+      const bool next = t + 1 < p.nsteps;
+      // every block needs the token for the next step; block 0 also records
+      // it, and its collection proves all blocks read this launch's counter
+      if (!dead && (next || r.blk == 0)) {
+        float best;
+        int bi;
+        if (!gather_argmax(ncu, p.off_amax, tbase + PH * p.L, best, bi, p.err, err_code(W_AMAX, 0))) {
+          fail();
+        } else {
+          const int n = r.n0 + t;
+          if (r.blk == 0 && lane == 0 && p.greedy) {
+            p.tokens_out[p.src.tok_off + 1 + n] = bi;  // window position prompt_len + n
+            if (n < p.max_new) p.out_ids[n] = bi;
+            if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+            *p.step_out = n + 1;
+          }
+          if (next) {
+            // x of the next token = tok_emb[id] + pos_emb[pos + 1]
+            const int id = (unsigned)bi < (unsigned)p.V ? bi : 0;
+            const float* te = p.tok + (size_t)id * D;
+            const float* pe = p.pos + (size_t)(r.pos0 + t + 1) * D;
+#pragma unroll
+            for (int c = 0; c < S::KC; c++) {
+              const int i = c * 256 + lane * 4;
+              const float4 a = *reinterpret_cast<const float4*>(te + i);
+              const float4 b = *reinterpret_cast<const float4*>(pe + i);
+              *reinterpret_cast<float4*>(sh.xres + i) = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+            }
+          }
+        }
+      }
+      __syncthreads();  // the next token's x is in xres
+    }
   }
 #undef TM
+  // all tokens done: block 0 advances the launch counter past this launch's tags
+  if (!dead && r.blk == 0 && lane == 0)
+    __hip_atomic_fetch_add(p.launch, (unsigned)p.nsteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Data waves: weight tiles in registers.  Each tile is requested right after
@@ -661,7 +734,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
 #define FH_MEARLY_NON 1
 #endif
 template <int D, int H, bool ATTN>
-__device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const Role& r) {
+__device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role r) {
   using S = Shape<D, H>;
   using U = Xu<D>;
   using XL = Xl<D, H>;
@@ -719,12 +792,12 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vc + (real ? hoff : 0), bytes);
     const int off = r.key0 * 256 + lane * 16;
 #pragma unroll
-    for (int i = 0; i < NKV; i++) kr[i] = ld4(rk, off + 1024 * i);
+    for (int i = 0; i < NKV; i++) kr[i] = ld4_l2(rk, off + 1024 * i);
 #pragma unroll
-    for (int i = 0; i < NKV; i++) vr[i] = ld4(rv, off + 1024 * i);
+    for (int i = 0; i < NKV; i++) vr[i] = ld4_l2(rv, off + 1024 * i);
   };
 #define TD(i) \
-  if (l == 1) trace_mark_d(p.trace, sh.trd, (i))
+  if (it == 1) trace_mark_d(p.trace, sh.trd, (i))
 #define DSYNC()    \
   __syncthreads(); \
   dead = sh.fail != 0
@@ -732,12 +805,19 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
   // Iteration l = -1 only requests layer 0's tiles, through the same load
   // statements as every later layer: each tile register has a single load
   // site, so no copy of an in-flight register (and no wait for it) is needed.
-  for (int l = -1; l < p.L; l++) {
-    const bool run = l >= 0;
-    const unsigned tb = r.tagbase + PH * l;
+  // tokens t < nsteps, layers l < L: one flat loop; iteration -1 only requests tiles
+  const int total = p.nsteps * p.L;
+  for (int it = -1; it < total; it++) {
+    const bool run = it >= 0;
+    const int t = run ? it / p.L : 0, l = run ? it - t * p.L : -1;
+    r.pos = r.pos0 + t;
+    r.nk = r.pos + 1;
+    r.wave_keys = ATTN && r.key0 < r.nk;
+    const unsigned tb = r.tag0 + (unsigned)t * TAGS + PH * l;
     const unsigned tA = tb, tC = tb + 3, tD = tb + 5, tE = tb + 6;
-    const bool more = l + 1 < p.L;
-    const int ln = more ? l + 1 : l;
+    const bool more = it + 1 < total;
+    const int ln = l + 1 < p.L ? l + 1 : 0;  // the next layer (the next token's first after the last)
+    const bool keys_next = r.key0 < (l + 1 < p.L ? r.nk : r.nk + 1);
     // ---- A: LN1 + QKV ----
     if (run) {
       DSYNC();
@@ -784,7 +864,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
     if constexpr (!ATTN) {
       load_q(ln, more);
       reload_fence();
-      if (l == 1 && p.trace) {  // trace: when this wave's requested tiles have landed
+      if (it == 1 && p.trace) {  // trace: when this wave's requested tiles have landed
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         TD(10);
       }
@@ -806,7 +886,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
           const float4 vnew = *reinterpret_cast<const float4*>(sh.qkvs + 128 + d4);
           float sc[NKV];
           float mloc = -INFINITY;
-          if (l == 1 && p.trace) {  // trace: wait for the K/V rows before timing the scores
+          if (it == 1 && p.trace) {  // trace: wait for the K/V rows before timing the scores
             float z = kr[0].x + vr[NKV - 1].w;
             asm volatile("" : "+v"(z));
             if (z == 1234.5f) mloc = 0.f;
@@ -863,7 +943,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
         __syncthreads();  // wm / wl / wo are complete
         __syncthreads();  // the control wave has published the block's partial
       }
-      load_kv(ln, more && r.wave_keys);
+      load_kv(ln, more && keys_next);
       reload_fence();
     }
     // ---- C: this XCD's part of attn.proj over its heads' o ----
@@ -943,6 +1023,74 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, const
       load_m(ln, more);
       reload_fence();
     }
+    if (run && l == p.L - 1) {
+      // ---- head of token t: LN_f + tied projection over this block's vocab rows ----
+      __syncthreads();  // the final x is in xres
+      dead = sh.fail != 0;
+      const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
+      constexpr int HG = 2;    // rows per wave in flight
+      const float* E = p.tok + (size_t)r.blk * R * D;
+      const int nrow = (R - w + NDW - 1) / NDW;
+      if (!dead) {
+        float4 rh[HG * KC];
+#pragma unroll
+        for (int u = 0; u < HG; u++) {
+          const int row = w + NDW * min(u, nrow - 1);
+#pragma unroll
+          for (int c = 0; c < KC; c++)
+            rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+        }
+        float4 xn[KC];
+        {
+          float4 lw[KC], lb[KC];
+#pragma unroll
+          for (int c = 0; c < KC; c++) {
+            lw[c] = *reinterpret_cast<const float4*>(sh.lnf + c * 256 + lane * 4);
+            lb[c] = *reinterpret_cast<const float4*>(sh.lnf + D + c * 256 + lane * 4);
+          }
+          ln_lane<KC, D>(sh.xres, lw, lb, xn);
+        }
+        for (int g = 0; g < nrow; g += HG) {
+          float4 nx[HG * KC];
+#pragma unroll
+          for (int u = 0; u < HG; u++) {
+            const int row = w + NDW * min(g + HG + u, nrow - 1);
+#pragma unroll
+            for (int c = 0; c < KC; c++)
+              nx[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+          }
+#pragma unroll
+          for (int u = 0; u < HG; u++) {
+            if (g + u < nrow) {
+              float acc = 0.f;
+#pragma unroll
+              for (int c = 0; c < KC; c++) acc += dot4(rh[u * KC + c], xn[c]);
+              const float v = wave_sum_dpp(acc);
+              if (lane == 0) sh.hval[w + NDW * (g + u)] = v;
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
+        }
+      }
+      __syncthreads();  // hval holds this block's logits
+      if (!dead && w == 0) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        if (lane < R) {
+          const float sv = sh.hval[lane];
+          const int v = r.blk * R + lane;
+          p.logits[v] = sv;
+          best = sv;
+          bi = v;
+        }
+        wave_argmax(best, bi);
+        if (lane == 0)
+          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
+              make_uint4(__float_as_uint(best), (unsigned)bi, r.tag0 + (unsigned)t * TAGS + PH * p.L, 0u);
+      }
+      __syncthreads();  // the next token's x is in xres
+    }
   }
 #undef TD
 #undef DSYNC
@@ -952,7 +1100,6 @@ template <int D, int H>
 __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   using S = Shape<D, H>;
   using XL = Xl<D, H>;
-  constexpr int KC = S::KC;
   __shared__ Lds<D, H> sh;
 
   Role r;
@@ -974,12 +1121,15 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   if (tid == 0) sh.fail = 0;
   if (tid < 16) sh.trd[tid] = 0ull;
   if (p.trace && tid == NT - 64) p.trace[r.blk * TRACE_PER + 12] = (unsigned long long)r.xcd;
-  r.tagbase = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
+  r.tag0 = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
   trace_mark(p.trace, 30);
 
-  const int n = *p.src.step;
-  r.pos = p.src.pos_off + p.src.pos_mul * n;  // position of the new token (>= 1)
-  int tokid = p.src.tokens[p.src.tok_off + n];
+  // steps n0 .. n0 + nsteps - 1 at positions pos0 ..
+  r.n0 = *p.src.step;
+  r.pos0 = p.src.pos_off + p.src.pos_mul * r.n0;  // position of the first new token (>= 1)
+  r.pos = r.pos0;
+  r.nk = r.pos0 + 1;
+  int tokid = p.src.tokens[p.src.tok_off + r.n0];
   if ((unsigned)tokid >= (unsigned)p.V) tokid = 0;
   r.xl = p.xl + (size_t)r.xcd * XL::STRIDE;
   r.xl0 = r.xcd * XL::STRIDE;
@@ -988,22 +1138,24 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   r.nh = (H - r.xcd + NX - 1) / NX;
   r.qc = 3 * S::HD * r.nh / SLOTS;
   r.qcw = r.qc / NDW;
-  // attention role: local head hj = slot / SPH, key block kb = slot % SPH
+  // attention role: local head hj = slot / SPH, key block kb = slot % SPH; the
+  // roles cover the keys of the launch's last token (earlier tokens leave the
+  // last blocks without keys: they publish empty partials)
   r.hj = r.slot / S::SPH;
   r.kb = r.slot % S::SPH;
   r.ah = r.xcd + NX * r.hj;
-  r.nk = r.pos + 1;
-  r.nkb = (r.nk + KPB - 1) / KPB;
+  r.nkb = (r.pos0 + p.nsteps + KPB - 1) / KPB;
   const bool attn_blk = r.hj < r.nh && r.kb < r.nkb;
   r.key0 = r.kb * KPB + r.w * KPW;
   r.wave_keys = attn_blk && r.key0 < r.nk;
 
-  // x = tok_emb[id] + pos_emb[pos] (every block keeps its own copy)
-  for (int i = tid; i < D; i += NT) sh.xres[i] = p.tok[(size_t)tokid * D + i] + p.pos[(size_t)r.pos * D + i];
+  // x = tok_emb[id] + pos_emb[pos] (every block keeps its own copy); ln_f
+  for (int i = tid; i < D; i += NT) sh.xres[i] = p.tok[(size_t)tokid * D + i] + p.pos[(size_t)r.pos0 * D + i];
+  for (int i = tid; i < 2 * D; i += NT) sh.lnf[i] = p.vecs[i];
 
   // The control wave and the data waves run separate loops, specialised by
-  // the block's role, that meet at the same sequence of barriers; a failed
-  // wait makes every wave leave at the next barrier.
+  // the block's role, that meet at the same sequence of barriers; after a
+  // failed wait every wave runs on to the end without waiting or storing.
   if (ctrl) {
     ctrl_loop<D, H>(p, sh, r, attn_blk);
   } else {
@@ -1012,126 +1164,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     else
       data_loop<D, H, false>(p, sh, r);
   }
-  const int lane = r.lane, w = r.w;
-  const unsigned tH = r.tagbase + PH * p.L;
-  if (ctrl) {
-    // ---- head: the final x ----
-    const NcBuf ncu(p.uc, p.uc_bytes);
-    const LcBuf ncl(p.xl, p.xl_bytes);
-    if (!sh.fail &&
-        !gather<D>(ncl, r.xl0 + XL::X, r.tagbase + PH * (p.L - 1) + 7, sh.xres, p.err, err_code(W_XF, 0)))
-      sh.fail = 1;
-    __syncthreads();
-    if (!sh.fail) {
-      __syncthreads();  // hval holds this block's logits
-      // block 0 collects every block's argmax: it proves all blocks read this
-      // launch's counter, so the counter can advance
-      if (r.blk == 0) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        long it = 0;
-        bool good = true;
-        for (;;) {
-          reload_fence();
-          bool okk = true;
-          best = -INFINITY;
-          bi = 0x7fffffff;
-#pragma unroll
-          for (int i = 0; i < NB / 64; i++) {
-            const uint4 a = ncu.load4(p.off_amax + 16 * (i * 64 + lane));
-            okk &= a.z == tH;
-            argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
-          }
-          if (__all(okk)) break;
-          if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
-            if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_AMAX, 0));
-            good = false;
-            break;
-          }
-        }
-        if (good) {
-          wave_argmax(best, bi);
-          if (lane == 0) {
-            if (p.greedy) {
-              const int total = p.src.tok_off + 1 + n;  // prompt_len + n
-              p.tokens_out[total] = bi;
-              if (n < p.max_new) p.out_ids[n] = bi;
-              if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
-              *p.step_out = n + 1;
-            }
-            __hip_atomic_fetch_add(p.launch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-        }
-      }
-    }
-  } else {
-    // ---- head: LN_f + tied projection over this block's vocab rows ----
-    const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
-    constexpr int HG = 4;    // rows per wave in flight
-    const float* E = p.tok + (size_t)r.blk * R * D;
-    float4 lnw[KC], lnb[KC];
-    {
-      const __amdgpu_buffer_rsrc_t rw = make_rsrc(p.vecs, D * 4), rb = make_rsrc(p.vecs + D, D * 4);
-#pragma unroll
-      for (int c = 0; c < KC; c++) {
-        lnw[c] = ld4(rw, c * 1024 + lane * 16);
-        lnb[c] = ld4(rb, c * 1024 + lane * 16);
-      }
-    }
-    float4 rh[HG * KC];
-    const int nrow = (R - w + NDW - 1) / NDW;  // rows of this wave
-#pragma unroll
-    for (int t = 0; t < HG; t++) {
-      const int row = w + NDW * min(t, nrow - 1);
-#pragma unroll
-      for (int c = 0; c < KC; c++)
-        rh[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
-    }
-    __syncthreads();
-    if (!sh.fail) {
-      float4 xn[KC];
-      ln_lane<KC, D>(sh.xres, lnw, lnb, xn);
-      for (int g = 0; g < nrow; g += HG) {
-        float4 nx[HG * KC];
-#pragma unroll
-        for (int t = 0; t < HG; t++) {
-          const int row = w + NDW * min(g + HG + t, nrow - 1);
-#pragma unroll
-          for (int c = 0; c < KC; c++)
-            nx[t * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
-        }
-#pragma unroll
-        for (int t = 0; t < HG; t++) {
-          if (g + t < nrow) {
-            float acc = 0.f;
-#pragma unroll
-            for (int c = 0; c < KC; c++) acc += dot4(rh[t * KC + c], xn[c]);
-            const float v = wave_sum_dpp(acc);
-            if (lane == 0) sh.hval[w + NDW * (g + t)] = v;
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
-      }
-      __syncthreads();
-      if (w == 0) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        if (lane < R) {
-          const float s = sh.hval[lane];
-          const int v = r.blk * R + lane;
-          p.logits[v] = s;
-          best = s;
-          bi = v;
-        }
-        wave_argmax(best, bi);
-        if (lane == 0)
-          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
-              make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
-      }
-    }
-  }
-  if (ctrl && p.trace && lane < 14) p.trace[r.blk * TRACE_PER + 16 + lane] = sh.trd[lane];
+  if (ctrl && p.trace && r.lane < 14) p.trace[r.blk * TRACE_PER + 16 + r.lane] = sh.trd[r.lane];
   trace_mark(p.trace, 31);
 }
 
@@ -1391,7 +1424,7 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
 int FastDecode::enqueue(hipStream_t st, const Step& s) {
   if (!enabled) return FH_ERR_STATE;
   if (!s.src.tokens || !s.src.step || !s.tokens || !s.step || !s.kcache || !s.vcache || !s.logits || !s.out_ids ||
-      !s.out_counts || s.src.pos_mul != 1 || s.max_new <= 0)
+      !s.out_counts || s.src.pos_mul != 1 || s.max_new <= 0 || s.nsteps < 1 || (s.nsteps > 1 && !s.greedy))
     return FH_ERR_INVALID;
   KParams k{};
   k.src = s.src;
@@ -1418,6 +1451,7 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.max_new = s.max_new;
   k.eos = s.eos;
   k.greedy = s.greedy;
+  k.nsteps = s.nsteps;
   k.tokens_out = s.tokens;
   k.step_out = s.step;
   k.trace = trace;

@@ -44,6 +44,8 @@ struct FastDecode {
     int max_new;
     int eos;
     int greedy;          // 1: argmax + history update inside the kernel
+    int nsteps = 1;      // steps run by the launch (more than one needs greedy): step
+                         // n + 1 starts from the argmax of step n, without the host
     int* tokens;         // mutable views of src.tokens / src.step
     int* step;
   };

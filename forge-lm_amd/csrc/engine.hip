@@ -382,6 +382,31 @@ int enqueue_window_step(fh_session* s, int T, const StepPlan& p) {
   return FH_OK;
 }
 
+// The fused kernel's greedy mode: no repetition controls, no logits dump.
+bool fused_greedy(const fh_session* s, const fh_sampling* o) {
+  return s->use_fast() && !(o->temperature > 0.f) && o->repetition_penalty == 1.f && o->no_repeat_ngram == 0 &&
+         s->dump == nullptr;
+}
+
+FastDecode::Step fused_step(fh_session* s, const StepPlan& p, int greedy, int nsteps) {
+  FastDecode::Step fs{};
+  fs.src = RowSrc{s->tokens, s->step, p.tok_stride, p.P - 1, p.P - 1, 1};
+  fs.tok_emb = s->v(s->idx_tok());
+  fs.pos_emb = s->v(s->idx_pos());
+  fs.kcache = reinterpret_cast<float*>(s->kc);
+  fs.vcache = reinterpret_cast<float*>(s->vc);
+  fs.logits = s->logits;
+  fs.out_ids = s->out_ids;
+  fs.out_counts = s->out_counts;
+  fs.max_new = p.max_new;
+  fs.eos = p.opts->eos_id;
+  fs.greedy = greedy;
+  fs.nsteps = nsteps;
+  fs.tokens = s->tokens;
+  fs.step = s->step;
+  return fs;
+}
+
 // One cached decode step: the token sampled last step at position P-1+n.
 template <typename WT>
 int enqueue_decode_step(fh_session* s, const StepPlan& p) {
@@ -391,23 +416,8 @@ int enqueue_decode_step(fh_session* s, const StepPlan& p) {
   if (s->use_fast()) {
     // greedy without repetition controls or a logits dump: the argmax runs
     // inside the decode kernel and no sampler launch follows
-    const bool greedy = !(p.opts->temperature > 0.f) && p.opts->repetition_penalty == 1.f &&
-                        p.opts->no_repeat_ngram == 0 && s->dump == nullptr;
-    FastDecode::Step fs{};
-    fs.src = src;
-    fs.tok_emb = s->v(s->idx_tok());
-    fs.pos_emb = s->v(s->idx_pos());
-    fs.kcache = reinterpret_cast<float*>(s->kc);
-    fs.vcache = reinterpret_cast<float*>(s->vc);
-    fs.logits = s->logits;
-    fs.out_ids = s->out_ids;
-    fs.out_counts = s->out_counts;
-    fs.max_new = p.max_new;
-    fs.eos = p.opts->eos_id;
-    fs.greedy = greedy ? 1 : 0;
-    fs.tokens = s->tokens;
-    fs.step = s->step;
-    int rc = s->fast.enqueue(st, fs);
+    const bool greedy = fused_greedy(s, p.opts);
+    int rc = s->fast.enqueue(st, fused_step(s, p, greedy ? 1 : 0, 1));
     if (rc != FH_OK) return set_err(rc, "fused decode step launch failed: %s", hipGetErrorString(hipGetLastError()));
     if (greedy) return FH_OK;
   } else {
@@ -947,7 +957,10 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   for (int n = 1; n < max_new; n++) (P + n > C ? n_re : n_dec)++;
   if (s->use_fast() && n_dec > 0 && s->fast.before_launches(n_dec) != FH_OK)
     return set_err(FH_ERR_HIP, "resetting the fused decode state failed");
-  if (n_dec > 0) {
+  // greedy on the fused kernel: one launch runs every cached step (the argmax
+  // of a step feeds the next inside the kernel); otherwise one graph per step
+  const bool persistent = n_dec > 0 && fused_greedy(s, opts);
+  if (n_dec > 0 && !persistent) {
     GraphKey k = key;
     k.kind = 0;
     rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, plan); });
@@ -961,7 +974,13 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
     (void)hipEventRecord(s->ev[0], st);
     rc = enqueue_window(s, T0, plan);
     (void)hipEventRecord(s->ev[1], st);
-    for (int n = 1; rc == FH_OK && n < max_new; n++) {
+    int n = 1;
+    if (rc == FH_OK && persistent) {
+      rc = s->fast.enqueue(st, fused_step(s, plan, 1, n_dec));
+      if (rc != FH_OK) rc = set_err(rc, "fused decode launch failed: %s", hipGetErrorString(hipGetLastError()));
+      n += n_dec;
+    }
+    for (; rc == FH_OK && n < max_new; n++) {
       hipError_t e = hipGraphLaunch(P + n > C ? s->g_reprefill.exec : s->g_decode.exec, st);
       if (e != hipSuccess) rc = set_err(FH_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
     }
