@@ -7,9 +7,10 @@ PCG32(42) prompt, 256 greedy tokens with the KV cache, random-init weights
 the timed region; only the 256 ids come back per step.
 
 value = generated tokens / wall time of the K timed steps (prefill included).
-roofline: the decode step's algorithmic HBM bytes (every weight once + the KV
-rows read and written + two embedding rows) over its average duration, timed
-with HIP events on the session stream inside the library.
+roofline: the decode kernel's algorithmic HBM bytes per launch (per token:
+every weight once + the KV rows read and written + two embedding rows; one
+fused launch runs all 255 cached greedy steps) over its duration, timed with
+HIP events on the session stream inside the library.
 cpu_baseline: the oracle's restatement of the reference CPU algorithm
 (full-window recompute per token, Sampler.Generate semantics) on this host,
 on the first tokens of the same workload.
@@ -140,6 +141,9 @@ def main():
     value = args.steps * NEW_TOKENS / wall
     fused = os.environ.get("FORGE_HIP_FUSED_DECODE", "1") != "0"
     kernel = "k_decode_step<768>" if fused else "decode step graph (generic kernels)"
+    # the fused greedy path runs every cached step in one launch; the generic
+    # path launches one graph per step
+    tokens_per_launch = n_dec if fused else 1
     out = {
         "metric": "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)",
         "value": round(value, 2),
@@ -162,8 +166,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": profiled_traffic(kernel) if fused else None,
-                     "kernel": kernel, "bytes_per_launch": int(step_bytes),
-                     "launch_us": round(avg_step_s * 1e6, 2)},
+                     "kernel": kernel, "tokens_per_launch": tokens_per_launch,
+                     "bytes_per_launch": int(step_bytes * tokens_per_launch),
+                     "launch_us": round(avg_step_s * tokens_per_launch * 1e6, 2)},
         "device": be.device_name,
     }
     if not args.no_cpu:

@@ -164,7 +164,8 @@ struct Xl {
   static constexpr int X2 = PARTS + S::HPX * S::SPH * PART;       // x2 (every XCD keeps a copy)
   static constexpr int HH = X2 + D;                               // the XCD's h slice
   static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
-  static constexpr int STRIDE = X + D;
+  static constexpr int ARG = X + D;                               // the XCD's 32 argmax records (2 pairs each)
+  static constexpr int STRIDE = ARG + 2 * SLOTS;
 };
 
 struct KParams {
@@ -195,7 +196,7 @@ struct KParams {
 
 // Optional timestamps (FORGE_HIP_TRACE=1): TRACE_PER entries per block, written
 // by the control wave (marks 0..15, 30, 31) and data wave 0 (marks 16..29).
-constexpr int TRACE_PER = 32;
+constexpr int TRACE_PER = 64;  // control wave marks [0, 32), data wave 0 marks [32, 64)
 __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
   if (t && threadIdx.x == (NT - 64)) t[blockIdx.x * TRACE_PER + i] = wall_clock64();
 }
@@ -477,7 +478,7 @@ struct Lds {
   float bias_s[2][S::BT];
   float hval[S::RMAX];
   __align__(16) float lnf[2 * D];  // ln_f weight, bias
-  unsigned long long trd[16];  // data wave 0's trace marks (0..13)
+  unsigned long long trd[32];  // data wave 0's trace marks
   int fail;
 };
 
@@ -492,6 +493,7 @@ struct Role {
   int key0;             // this data wave's first key
   bool wave_keys;
   unsigned tag0;        // tag base of the launch's first token
+  int trace_it;         // token/layer iteration the trace marks (token 5, layer 1 when there is one)
   uint2* xl;            // this XCD's local pairs
   int xl0;              // same, as a pair index into p.xl
 };
@@ -501,22 +503,20 @@ struct Role {
 // failed wait (sh.fail) it skips the remaining waits and stores but meets
 // every barrier: the loops have no early exit, which keeps the compiler's
 // load-wait bookkeeping exact across iterations.
-// Control wave, head of a token: waits until every block's argmax record carries
-// `tag`, then returns the overall (first) maximum in best / bi.
-__device__ bool gather_argmax(const NcBuf& nc, int off, unsigned tag, float& best, int& bi, int* err, int code) {
+// Control wave, head of a token: waits until the NR argmax records (value, index,
+// tag, 0) at byte offset `off` all carry `tag`, then returns their (first)
+// maximum in best / bi.
+template <int NR, typename B>
+__device__ bool gather_argmax(const B& nc, int off, unsigned tag, float& best, int& bi, int* err, int code) {
+  static_assert(NR <= 64, "one record per lane");
   const int lane = threadIdx.x & 63;
   long it = 0;
   for (;;) {
     reload_fence();
-    bool ok = true;
-    best = -INFINITY;
-    bi = 0x7fffffff;
-#pragma unroll
-    for (int i = 0; i < NB / 64; i++) {
-      const uint4 a = nc.load4(off + 16 * (i * 64 + lane));
-      ok &= a.z == tag;
-      argmax_merge(best, bi, __uint_as_float(a.x), (int)a.y);
-    }
+    const uint4 a = nc.load4(off + 16 * min(lane, NR - 1));
+    const bool ok = lane >= NR || a.z == tag;
+    best = lane < NR ? __uint_as_float(a.x) : -INFINITY;
+    bi = lane < NR ? (int)a.y : 0x7fffffff;
     if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
       if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
@@ -544,7 +544,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     sh.fail = 1;
   };
 #define TM(i) \
-  if (it == 1) trace_mark(p.trace, (i))
+  if (it == r.trace_it) trace_mark(p.trace, (i))
   // tokens t < nsteps, layers l < L: one flat loop
   const int total = p.nsteps * p.L;
   for (int it = 0; it < total; it++) {
@@ -558,7 +558,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       fail();
     __syncthreads();
     TM(0);
-    if (it == 2) trace_mark(p.trace, 9);
+    if (it == r.trace_it + 1) trace_mark(p.trace, 9);
     // Every phase whose data waves publish and then request tiles has a
     // second barrier between the two, so that no published value queues
     // behind the tile loads of another wave of this CU.
@@ -592,9 +592,9 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     // ---- C: o of the XCD's heads from every key block's partial ----
     if (!dead &&
         !gather_parts<D, H>(ncl, r.xl0 + XL::PARTS, r.nh, r.nkb, tP, sh.parts, p.err, err_code(W_PART, l), &np[2],
-                            (it == 1 && p.trace) ? &tfirst : nullptr))
+                            (it == r.trace_it && p.trace) ? &tfirst : nullptr))
       fail();
-    if (it == 1 && p.trace) tdone = wall_clock64();
+    if (it == r.trace_it && p.trace) tdone = wall_clock64();
     if (!dead) {
       // DPP row j (lanes 16j .. 16j+15) holds head j's partials, lane 16j + c
       // partial c: its weight exp(m - M_j) goes to sh.pw, the row sums l * weight;
@@ -626,7 +626,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         }
       }
     }
-    if (it == 1 && p.trace) tcomb = wall_clock64();
+    if (it == r.trace_it && p.trace) tcomb = wall_clock64();
     __syncthreads();
     TM(3);
     __syncthreads();
@@ -662,7 +662,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       put_pair(r.xl + XL::X + col, (sum + sh.bias_s[l & 1][S::B_M + lane]) + sh.x2s[col], tE2);
     }
     TM(6);
-    if (it == 1 && p.trace && lane == 0) {
+    if (it == r.trace_it && p.trace && lane == 0) {
       for (int i = 1; i < 3; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
       p.trace[r.blk * TRACE_PER + 14] = tfirst;
       p.trace[r.blk * TRACE_PER + 15] = tcomb;
@@ -671,15 +671,47 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     if (l == p.L - 1) {
       // ---- head of token t: the final x, this block's logits, every block's argmax ----
       if (!dead && !gather<D>(ncl, r.xl0 + XL::X, tb + 7, sh.xres, p.err, err_code(W_XF, 0))) fail();
+      const bool thead = it == r.trace_it + p.L - 2;  // the head of the traced token
+      if (thead) trace_mark(p.trace, 16);
       __syncthreads();  // x is in xres: the data waves compute this block's logits
-      __syncthreads();  // data wave 0 publishes the block's argmax record
+      __syncthreads();  // hval holds them
+      const unsigned tH = tbase + PH * p.L;
+      if (!dead) {
+        // this block's logits (for a host-side sampler) and its argmax record
+        const int R = p.V / NB;
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        if (lane < R) {
+          const float sv = sh.hval[lane];
+          const int v = r.blk * R + lane;
+          if (!p.greedy) p.logits[v] = sv;
+          best = sv;
+          bi = v;
+        }
+        wave_argmax(best, bi);
+        if (lane == 0)
+          *reinterpret_cast<uint4*>(r.xl + XL::ARG + 2 * r.slot) = make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
+      }
+      if (thead) trace_mark(p.trace, 17);
       const bool next = t + 1 < p.nsteps;
-      // every block needs the token for the next step; block 0 also records
-      // it, and its collection proves all blocks read this launch's counter
+      // Two levels: slot 0 of each XCD reduces the XCD's 32 records (in its L2)
+      // to one uncached record; every block then reduces the 8 of those.  Every
+      // block needs the token for the next step; block 0 also records it, and
+      // its collection proves all blocks read this launch's counter.
+      if (!dead && r.slot == 0) {
+        float best;
+        int bi;
+        if (!gather_argmax<SLOTS>(ncl, (r.xl0 + XL::ARG) * 8, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
+          fail();
+        } else if (lane == 0) {
+          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.xcd) =
+              make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
+        }
+      }
       if (!dead && (next || r.blk == 0)) {
         float best;
         int bi;
-        if (!gather_argmax(ncu, p.off_amax, tbase + PH * p.L, best, bi, p.err, err_code(W_AMAX, 0))) {
+        if (!gather_argmax<NX>(ncu, p.off_amax, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
           fail();
         } else {
           const int n = r.n0 + t;
@@ -689,6 +721,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
             if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
             *p.step_out = n + 1;
           }
+          if (thead) trace_mark(p.trace, 18);
           if (next) {
             // x of the next token = tok_emb[id] + pos_emb[pos + 1]
             const int id = (unsigned)bi < (unsigned)p.V ? bi : 0;
@@ -705,6 +738,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         }
       }
       __syncthreads();  // the next token's x is in xres
+      if (thead) trace_mark(p.trace, 19);
     }
   }
 #undef TM
@@ -797,7 +831,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
     for (int i = 0; i < NKV; i++) vr[i] = ld4_l2(rv, off + 1024 * i);
   };
 #define TD(i) \
-  if (it == 1) trace_mark_d(p.trace, sh.trd, (i))
+  if (it == r.trace_it) trace_mark_d(p.trace, sh.trd, (i))
 #define DSYNC()    \
   __syncthreads(); \
   dead = sh.fail != 0
@@ -864,7 +898,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
     if constexpr (!ATTN) {
       load_q(ln, more);
       reload_fence();
-      if (it == 1 && p.trace) {  // trace: when this wave's requested tiles have landed
+      if (it == r.trace_it && p.trace) {  // trace: when this wave's requested tiles have landed
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         TD(10);
       }
@@ -886,7 +920,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
           const float4 vnew = *reinterpret_cast<const float4*>(sh.qkvs + 128 + d4);
           float sc[NKV];
           float mloc = -INFINITY;
-          if (it == 1 && p.trace) {  // trace: wait for the K/V rows before timing the scores
+          if (it == r.trace_it && p.trace) {  // trace: wait for the K/V rows before timing the scores
             float z = kr[0].x + vr[NKV - 1].w;
             asm volatile("" : "+v"(z));
             if (z == 1234.5f) mloc = 0.f;
@@ -1073,22 +1107,8 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
           for (int i = 0; i < HG * KC; i++) rh[i] = nx[i];
         }
       }
+      if (it == r.trace_it + p.L - 2) trace_mark_d(p.trace, sh.trd, 14);
       __syncthreads();  // hval holds this block's logits
-      if (!dead && w == 0) {
-        float best = -INFINITY;
-        int bi = 0x7fffffff;
-        if (lane < R) {
-          const float sv = sh.hval[lane];
-          const int v = r.blk * R + lane;
-          p.logits[v] = sv;
-          best = sv;
-          bi = v;
-        }
-        wave_argmax(best, bi);
-        if (lane == 0)
-          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
-              make_uint4(__float_as_uint(best), (unsigned)bi, r.tag0 + (unsigned)t * TAGS + PH * p.L, 0u);
-      }
       __syncthreads();  // the next token's x is in xres
     }
   }
@@ -1119,12 +1139,13 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // virtual block id vb; the head rows are indexed by blk
   r.vb = r.slot * NX + r.xcd;
   if (tid == 0) sh.fail = 0;
-  if (tid < 16) sh.trd[tid] = 0ull;
+  if (tid < 32) sh.trd[tid] = 0ull;
   if (p.trace && tid == NT - 64) p.trace[r.blk * TRACE_PER + 12] = (unsigned long long)r.xcd;
   r.tag0 = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
   trace_mark(p.trace, 30);
 
   // steps n0 .. n0 + nsteps - 1 at positions pos0 ..
+  r.trace_it = p.nsteps > 5 ? 5 * p.L + 1 : 1;
   r.n0 = *p.src.step;
   r.pos0 = p.src.pos_off + p.src.pos_mul * r.n0;  // position of the first new token (>= 1)
   r.pos = r.pos0;
@@ -1164,7 +1185,7 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
     else
       data_loop<D, H, false>(p, sh, r);
   }
-  if (ctrl && p.trace && r.lane < 14) p.trace[r.blk * TRACE_PER + 16 + r.lane] = sh.trd[r.lane];
+  if (ctrl && p.trace && r.lane < 32) p.trace[r.blk * TRACE_PER + 32 + r.lane] = sh.trd[r.lane];
   trace_mark(p.trace, 31);
 }
 

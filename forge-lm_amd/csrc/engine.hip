@@ -1023,7 +1023,7 @@ int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n) {
   if (!s || !out || n < 0) return set_err(FH_ERR_INVALID, "bad argument");
   if (!s->fast.trace) return set_err(FH_ERR_STATE, "tracing is off (set FORGE_HIP_TRACE=1 before creating the session)");
   HIP_TRY(hipStreamSynchronize(s->ctx->stream));
-  HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256 * 32), hipMemcpyDeviceToHost));
+  HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256 * 64), hipMemcpyDeviceToHost));
   return FH_OK;
 }
 
