@@ -164,8 +164,7 @@ struct Xl {
   static constexpr int X2 = PARTS + S::HPX * S::SPH * PART;       // x2 (every XCD keeps a copy)
   static constexpr int HH = X2 + D;                               // the XCD's h slice
   static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
-  static constexpr int ARG = X + D;                               // the XCD's 32 argmax records (2 pairs each)
-  static constexpr int STRIDE = ARG + 2 * SLOTS;
+  static constexpr int STRIDE = X + D;
 };
 
 struct KParams {
@@ -200,45 +199,92 @@ constexpr int TRACE_PER = 64;  // control wave marks [0, 32), data wave 0 marks 
 __device__ __forceinline__ void trace_mark(unsigned long long* t, int i) {
   if (t && threadIdx.x == (NT - 64)) t[blockIdx.x * TRACE_PER + i] = wall_clock64();
 }
-// data wave 0 keeps its marks in LDS (a global store would make its next
-// wait for a tile cover every load in flight); the control wave writes them out
+// data wave 0 keeps its marks in LDS (no extra memory requests in the data
+// waves' queue); the control wave writes them out at the end
 __device__ __forceinline__ void trace_mark_d(unsigned long long* t, unsigned long long* lds, int i) {
   if (t && threadIdx.x == 0) lds[i] = wall_clock64();
 }
 
+#ifndef FH_POLL2
+#define FH_POLL2 0
+#endif
+// The poll loop of every gather: issue(v) requests R 16-byte values per lane,
+// good(v) says whether every tag matches (wave-uniform), take(v) stores them.
+// With FH_POLL2 a second read is requested before the first is checked, so a
+// poll result comes back about twice as often while reads wait behind the
+// CU's tile loads.
+template <int R, typename Issue, typename Good, typename Take>
+__device__ __forceinline__ bool poll(Issue issue, Good good, Take take, int* err, int code, long* npoll) {
+  const int lane = threadIdx.x & 63;
+  long it = 0;
+#if FH_POLL2
+  uint4 va[R], vb[R];
+  issue(va);
+  for (;;) {
+    issue(vb);
+    if (good(va)) {
+      take(va);
+      break;
+    }
+    issue(va);
+    if (good(vb)) {
+      take(vb);
+      break;
+    }
+    it += 2;
+    if ((it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
+      return false;
+    }
+  }
+#else
+  uint4 v[R];
+  for (;;) {
+    issue(v);
+    if (good(v)) {
+      take(v);
+      break;
+    }
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
+      return false;
+    }
+  }
+#endif
+  if (npoll) *npoll = it;
+  return true;
+}
+
 // Control wave: waits until pairs[pair0, pair0 + n) all carry `tag` (n <= N),
-// then stores the values to out[0, n) (LDS).  One read in flight: a second poll
-// issued ahead would still be in flight when the wait ends, and reusing its
-// registers would wait for it.
+// then stores the values to out[0, n) (LDS).
 template <int N, typename B>
 __device__ bool gather(const B& nc, int pair0, unsigned tag, float* out, int* err, int code, int n = N,
                        long* npoll = nullptr) {
   static_assert(N % 2 == 0, "pairs come in 16-byte loads");
   constexpr int R = (N + 127) / 128;
   const int lane = threadIdx.x & 63;
-  uint4 v[R];
-  long it = 0;
-  for (;;) {
-    reload_fence();
+  return poll<R>(
+      [&](uint4(&v)[R]) {
+        reload_fence();
 #pragma unroll
-    for (int r = 0; r < R; r++) v[r] = nc.load4(pair0 * 8 + (r * 64 + lane) * 16);
-    bool ok = true;
+        for (int r = 0; r < R; r++) v[r] = nc.load4(pair0 * 8 + (r * 64 + lane) * 16);
+      },
+      [&](const uint4(&v)[R]) {
+        bool ok = true;
 #pragma unroll
-    for (int r = 0; r < R; r++)
-      if ((r * 64 + lane) * 2 < n) ok &= (v[r].y == tag) & (v[r].w == tag);
-    if (__all(ok)) break;
-    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
-      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
-      return false;
-    }
-  }
-  if (npoll) *npoll = it;
+        for (int r = 0; r < R; r++)
+          if ((r * 64 + lane) * 2 < n) ok &= (v[r].y == tag) & (v[r].w == tag);
+        return __all(ok) != 0;
+      },
+      [&](const uint4(&v)[R]) {
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int i = 2 * (r * 64 + lane);
-    if (i < n) *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
-  }
-  return true;
+        for (int r = 0; r < R; r++) {
+          const int i = 2 * (r * 64 + lane);
+          if (i < n)
+            *reinterpret_cast<float2*>(out + i) = make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+        }
+      },
+      err, code, npoll);
 }
 
 // Control wave: the RSC-column slice [slot*RSC, +RSC) of all NX per-XCD partial
@@ -250,35 +296,33 @@ __device__ bool gather_slices(const NcBuf& nc, int pair0, int slot, unsigned tag
   constexpr int NQ = NX * Q;
   constexpr int R = (NQ + 63) / 64;
   const int lane = threadIdx.x & 63;
-  uint4 v[R];
-  long it = 0;
-  for (;;) {
-    reload_fence();
+  return poll<R>(
+      [&](uint4(&v)[R]) {
+        reload_fence();
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-      const int u = min(r * 64 + lane, NQ - 1), x = u / Q, q = u % Q;
-      v[r] = nc.load4((pair0 + x * D + slot * RSC + 2 * q) * 8);
-    }
-    bool ok = true;
+        for (int r = 0; r < R; r++) {
+          const int u = min(r * 64 + lane, NQ - 1), x = u / Q, q = u % Q;
+          v[r] = nc.load4((pair0 + x * D + slot * RSC + 2 * q) * 8);
+        }
+      },
+      [&](const uint4(&v)[R]) {
+        bool ok = true;
 #pragma unroll
-    for (int r = 0; r < R; r++) ok &= (v[r].y == tag) & (v[r].w == tag);
-    if (__all(ok)) break;
-    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
-      if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
-      return false;
-    }
-  }
-  if (npoll) *npoll = it;
+        for (int r = 0; r < R; r++) ok &= (v[r].y == tag) & (v[r].w == tag);
+        return __all(ok) != 0;
+      },
+      [&](const uint4(&v)[R]) {
 #pragma unroll
-  for (int r = 0; r < R; r++) {
-    const int u = r * 64 + lane;
-    if (u < NQ) {
-      const int x = u / Q, q = u % Q;
-      *reinterpret_cast<float2*>(out + x * RSC + 2 * q) =
-          make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
-    }
-  }
-  return true;
+        for (int r = 0; r < R; r++) {
+          const int u = r * 64 + lane;
+          if (u < NQ) {
+            const int x = u / Q, q = u % Q;
+            *reinterpret_cast<float2*>(out + x * RSC + 2 * q) =
+                make_float2(__uint_as_float(v[r].x), __uint_as_float(v[r].z));
+          }
+        }
+      },
+      err, code, npoll);
 }
 
 // sum over the 16 lanes of each DPP row (quad permutes, half-row and row mirrors)
@@ -317,7 +361,7 @@ __device__ __forceinline__ void ln_lane(const float* xin, const float4 (&w)[KC],
     xv[c] = *reinterpret_cast<const float4*>(xin + c * 256 + lane * 4);
     s += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
   }
-  const float mu = wave_sum_dpp(s) / (float)D;
+  const float mu = wave_sum_dpp(s) * (1.f / (float)D);
   float v = 0.f;
 #pragma unroll
   for (int c = 0; c < KC; c++) {
@@ -325,7 +369,7 @@ __device__ __forceinline__ void ln_lane(const float* xin, const float4 (&w)[KC],
     v += (a * a + bb * bb) + (cc * cc + dd * dd);
   }
   const float var = wave_sum_dpp(v);
-  const float rs = 1.f / sqrtf(var / (float)D + 1e-5f);
+  const float rs = __frsqrt_rn(var * (1.f / (float)D) + 1e-5f);
 #pragma unroll
   for (int c = 0; c < KC; c++) {
     xn[c].x = (xv[c].x - mu) * rs * w[c].x + b[c].x;
@@ -384,7 +428,7 @@ __device__ __forceinline__ float ln_center(const float* xin, float4 (&d)[KC]) {
     d[c] = *reinterpret_cast<const float4*>(xin + c * 256 + lane * 4);
     s += (d[c].x + d[c].y) + (d[c].z + d[c].w);
   }
-  const float mu = wave_sum_dpp(s) / (float)D;
+  const float mu = wave_sum_dpp(s) * (1.f / (float)D);
   float v = 0.f;
 #pragma unroll
   for (int c = 0; c < KC; c++) {
@@ -395,7 +439,7 @@ __device__ __forceinline__ float ln_center(const float* xin, float4 (&d)[KC]) {
     v += (d[c].x * d[c].x + d[c].y * d[c].y) + (d[c].z * d[c].z + d[c].w * d[c].w);
   }
   const float var = wave_sum_dpp(v);
-  return __frsqrt_rn(var / (float)D + 1e-5f);
+  return __frsqrt_rn(var * (1.f / (float)D) + 1e-5f);
 }
 
 // Control wave: the attention partials of the XCD's nh heads, nkb key blocks
@@ -508,15 +552,24 @@ struct Role {
 // maximum in best / bi.
 template <int NR, typename B>
 __device__ bool gather_argmax(const B& nc, int off, unsigned tag, float& best, int& bi, int* err, int code) {
-  static_assert(NR <= 64, "one record per lane");
+  constexpr int R = (NR + 63) / 64;  // records per lane
   const int lane = threadIdx.x & 63;
   long it = 0;
   for (;;) {
     reload_fence();
-    const uint4 a = nc.load4(off + 16 * min(lane, NR - 1));
-    const bool ok = lane >= NR || a.z == tag;
-    best = lane < NR ? __uint_as_float(a.x) : -INFINITY;
-    bi = lane < NR ? (int)a.y : 0x7fffffff;
+    uint4 a[R];
+#pragma unroll
+    for (int i = 0; i < R; i++) a[i] = nc.load4(off + 16 * min(i * 64 + lane, NR - 1));
+    bool ok = true;
+    best = -INFINITY;
+    bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < R; i++) {
+      if (i * 64 + lane < NR) {
+        ok &= a[i].z == tag;
+        argmax_merge(best, bi, __uint_as_float(a[i].x), (int)a[i].y);
+      }
+    }
     if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
       if (lane == 0 && it > SPIN_LIMIT) raise_err(err, code);
@@ -690,28 +743,19 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         }
         wave_argmax(best, bi);
         if (lane == 0)
-          *reinterpret_cast<uint4*>(r.xl + XL::ARG + 2 * r.slot) = make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
+          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
+              make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
       }
       if (thead) trace_mark(p.trace, 17);
       const bool next = t + 1 < p.nsteps;
-      // Two levels: slot 0 of each XCD reduces the XCD's 32 records (in its L2)
-      // to one uncached record; every block then reduces the 8 of those.  Every
-      // block needs the token for the next step; block 0 also records it, and
-      // its collection proves all blocks read this launch's counter.
-      if (!dead && r.slot == 0) {
-        float best;
-        int bi;
-        if (!gather_argmax<SLOTS>(ncl, (r.xl0 + XL::ARG) * 8, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
-          fail();
-        } else if (lane == 0) {
-          *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.xcd) =
-              make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
-        }
-      }
+      // Every block reduces the 256 uncached records itself (one hop; a two-level
+      // reduction through each XCD's L2 measured slower): every block needs the
+      // token for the next step; block 0 also records it, and its collection
+      // proves all blocks read this launch's counter.
       if (!dead && (next || r.blk == 0)) {
         float best;
         int bi;
-        if (!gather_argmax<NX>(ncu, p.off_amax, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
+        if (!gather_argmax<NB>(ncu, p.off_amax, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
           fail();
         } else {
           const int n = r.n0 + t;
@@ -755,17 +799,43 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
 // Every load is unconditional (an empty buffer resource past the last layer),
 // so each register has one producer and one consumer per iteration.  After a
 // failed wait (sh.fail, read after each barrier) the stores are skipped.
-#ifndef FH_FEARLY_ALL
-#define FH_FEARLY_ALL 0
+// Load sites of the data loop, in program order within a layer: after A's
+// puts, at the start of B and after B (attention blocks), after the puts of
+// C, D and E.  A tile requested before its use in the layer is the layer's
+// own; after its use, the next layer's (the next token's first after the last).
+#ifndef FH_HG
+#define FH_HG 3
 #endif
-#ifndef FH_MEARLY_ALL
-#define FH_MEARLY_ALL 0
+enum Site : int { S_AEND = 0, S_BSTART = 1, S_BEND = 2, S_CEND = 3, S_DEND = 4, S_EEND = 5 };
+// site of each tile: non-attention blocks request mlp.fc / mlp.proj / next qkv
+// right after A (their only slack is the attention window); attention blocks
+// spread theirs over the layer
+#ifndef FH_NQ
+#define FH_NQ S_AEND
 #endif
-#ifndef FH_FEARLY_NON
-#define FH_FEARLY_NON 1
+#ifndef FH_NP
+#define FH_NP S_CEND
 #endif
-#ifndef FH_MEARLY_NON
-#define FH_MEARLY_NON 1
+#ifndef FH_NF
+#define FH_NF S_AEND
+#endif
+#ifndef FH_NM
+#define FH_NM S_AEND
+#endif
+#ifndef FH_AQ
+#define FH_AQ S_BSTART
+#endif
+#ifndef FH_AKV
+#define FH_AKV S_BEND
+#endif
+#ifndef FH_AP
+#define FH_AP S_CEND
+#endif
+#ifndef FH_AF
+#define FH_AF S_DEND
+#endif
+#ifndef FH_AM
+#define FH_AM S_EEND
 #endif
 template <int D, int H, bool ATTN>
 __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role r) {
@@ -773,10 +843,11 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
   using U = Xu<D>;
   using XL = Xl<D, H>;
   constexpr int KC = S::KC, G = S::G;
-  // FEARLY / MEARLY: mlp.fc / mlp.proj tiles of layer l are requested right
-  // after A(l) instead of after their use in the previous layer
-  constexpr bool FEARLY = FH_FEARLY_ALL || (!ATTN && FH_FEARLY_NON);
-  constexpr bool MEARLY = FH_MEARLY_ALL || (!ATTN && FH_MEARLY_NON);
+  constexpr int SQ = ATTN ? FH_AQ : FH_NQ, SP = ATTN ? FH_AP : FH_NP, SF = ATTN ? FH_AF : FH_NF,
+                SM = ATTN ? FH_AM : FH_NM, SKV = FH_AKV;
+  static_assert(ATTN || (SQ != S_BSTART && SQ != S_BEND && SP != S_BSTART && SP != S_BEND && SF != S_BSTART &&
+                         SF != S_BEND && SM != S_BSTART && SM != S_BEND),
+                "blocks without attention have no phase B");
   const int w = r.w, lane = r.lane;
   float4 rq[S::QCW * KC], rp[S::PJ * G], rf[S::FCW * KC], rm[G * S::MJ];
   // K/V rows of this wave's keys: register i holds rows key0 + 4i .. key0 + 4i + 3,
@@ -852,6 +923,51 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
     const bool more = it + 1 < total;
     const int ln = l + 1 < p.L ? l + 1 : 0;  // the next layer (the next token's first after the last)
     const bool keys_next = r.key0 < (l + 1 < p.L ? r.nk : r.nk + 1);
+    // the requests of one site: this layer's tiles (in order of use), then the next layer's
+    auto site = [&](auto site_c) {
+      constexpr int X = decltype(site_c)::value;
+      const int lc = run ? l : 0;
+      if constexpr (ATTN) {
+        if constexpr (SKV == X && X < S_BSTART) {
+          load_kv(lc, run && r.wave_keys);
+          reload_fence();
+        }
+      }
+      if constexpr (SP == X && X < S_CEND) {
+        load_p(lc, run);
+        reload_fence();
+      }
+      if constexpr (SF == X && X < S_DEND) {
+        load_f(lc, run);
+        reload_fence();
+      }
+      if constexpr (SM == X && X < S_EEND) {
+        load_m(lc, run);
+        reload_fence();
+      }
+      if constexpr (SQ == X) {
+        load_q(ln, more);
+        reload_fence();
+      }
+      if constexpr (ATTN) {
+        if constexpr (SKV == X && X >= S_BSTART) {
+          load_kv(ln, more && keys_next);
+          reload_fence();
+        }
+      }
+      if constexpr (SP == X && X >= S_CEND) {
+        load_p(ln, more);
+        reload_fence();
+      }
+      if constexpr (SF == X && X >= S_DEND) {
+        load_f(ln, more);
+        reload_fence();
+      }
+      if constexpr (SM == X && X >= S_EEND) {
+        load_m(ln, more);
+        reload_fence();
+      }
+    };
     // ---- A: LN1 + QKV ----
     if (run) {
       DSYNC();
@@ -884,24 +1000,10 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       }
       __syncthreads();  // every put of the phase is issued before any tile load
     }
-    // early tiles of this layer (l = -1: nothing), then the next layer's qkv
-    if constexpr (FEARLY) {
-      load_f(run ? l : 0, run);
-      reload_fence();  // keeps the issue order of the tiles (the first iteration has no barriers)
-    }
-    if constexpr (MEARLY) {
-      load_m(run ? l : 0, run);
-      reload_fence();
-    }
-    // attention blocks request the next qkv tile once their own q/k/v have
-    // arrived (a queue of tile loads would delay that hand-off)
-    if constexpr (!ATTN) {
-      load_q(ln, more);
-      reload_fence();
-      if (it == r.trace_it && p.trace) {  // trace: when this wave's requested tiles have landed
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        TD(10);
-      }
+    site(std::integral_constant<int, S_AEND>());
+    if (!ATTN && it == r.trace_it && p.trace) {  // trace: when this wave's requested tiles have landed
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      TD(10);
     }
     // ---- B: attention of head ah over key block kb ----
     if constexpr (ATTN) {
@@ -909,8 +1011,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
         DSYNC();
         TD(2);
       }
-      load_q(ln, more);
-      reload_fence();
+      site(std::integral_constant<int, S_BSTART>());
       if (run) {
         if (r.wave_keys) {
           // lane l: dims 4*(l % 16) .. +3 of keys key0 + 4i + l / 16, i < KPW / 4
@@ -977,8 +1078,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
         __syncthreads();  // wm / wl / wo are complete
         __syncthreads();  // the control wave has published the block's partial
       }
-      load_kv(ln, more && keys_next);
-      reload_fence();
+      site(std::integral_constant<int, S_BEND>());
     }
     // ---- C: this XCD's part of attn.proj over its heads' o ----
     if (run) {
@@ -1003,8 +1103,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       }
       __syncthreads();  // every put of the phase is issued before any tile load
     }
-    load_p(ln, more);
-    reload_fence();
+    site(std::integral_constant<int, S_CEND>());
     // ---- D: LN2 + mlp.fc + GELU -> this XCD's h slice ----
     if (run) {
       DSYNC();
@@ -1029,10 +1128,7 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       }
       __syncthreads();  // every put of the phase is issued before any tile load
     }
-    if constexpr (!FEARLY) {
-      load_f(ln, more);
-      reload_fence();
-    }
+    site(std::integral_constant<int, S_DEND>());
     // ---- E: this XCD's part of mlp.proj over its h slice ----
     if (run) {
       DSYNC();
@@ -1053,27 +1149,25 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       }
       __syncthreads();  // every put of the phase is issued before any tile load
     }
-    if constexpr (!MEARLY) {
-      load_m(ln, more);
-      reload_fence();
-    }
+    site(std::integral_constant<int, S_EEND>());
     if (run && l == p.L - 1) {
       // ---- head of token t: LN_f + tied projection over this block's vocab rows ----
-      __syncthreads();  // the final x is in xres
-      dead = sh.fail != 0;
       const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
-      constexpr int HG = 2;    // rows per wave in flight
+      constexpr int HG = FH_HG;  // rows per wave in flight
       const float* E = p.tok + (size_t)r.blk * R * D;
       const int nrow = (R - w + NDW - 1) / NDW;
+      // the first rows are requested before the final x arrives
+      float4 rh[HG * KC];
+#pragma unroll
+      for (int u = 0; u < HG; u++) {
+        const int row = w + NDW * min(u, nrow - 1);
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+          rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+      }
+      __syncthreads();  // the final x is in xres
+      dead = sh.fail != 0;
       if (!dead) {
-        float4 rh[HG * KC];
-#pragma unroll
-        for (int u = 0; u < HG; u++) {
-          const int row = w + NDW * min(u, nrow - 1);
-#pragma unroll
-          for (int c = 0; c < KC; c++)
-            rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
-        }
         float4 xn[KC];
         {
           float4 lw[KC], lb[KC];
