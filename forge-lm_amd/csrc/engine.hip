@@ -287,6 +287,21 @@ int linear(fh_session* s, const float* x, int M, int K, size_t slot, int N, cons
   return FH_OK;
 }
 
+// Tied head for B rows: logits = xn @ tok_emb^T.  tok_emb [V][d] is already
+// the transposed operand the MFMA GEMM reads, so more than 4 rows go there.
+template <typename WT>
+int head(fh_session* s, int B) {
+  hipStream_t st = s->ctx->stream;
+  const int D = s->d.d_model, V = s->d.vocab_size;
+  if (B > 4 && D % 32 == 0) {
+    LAUNCH(launch_gemm_mfma<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), V, nullptr, EPI_NONE, nullptr, s->logits,
+                                s->part, s->part_floats, s->ctx->props.multiProcessorCount));
+  } else {
+    LAUNCH(launch_head<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), V, s->logits));
+  }
+  return FH_OK;
+}
+
 template <typename WT>
 int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
   hipStream_t st = s->ctx->stream;
@@ -323,7 +338,10 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 2), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, 1, D, H, C, kc, vc));
-    LAUNCH(launch_attn_decode<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, 64, s->o));
+    if (D == 64 * H)
+      LAUNCH(launch_attn_decode_wide<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, s->o));
+    else
+      LAUNCH(launch_attn_decode<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, 64, s->o));
     FH_TRY(linear<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
     LAUNCH(launch_layernorm(st, s->x2, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
     FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
@@ -377,7 +395,7 @@ int enqueue_window_step(fh_session* s, int T, const StepPlan& p) {
   FH_TRY(enqueue_layers_window<WT>(s, T, src));
   const size_t lf = s->idx_lnf();
   LAUNCH(launch_layernorm(st, s->x, B, 1, T, T - 1, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
-  LAUNCH(launch_head<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), s->d.vocab_size, s->logits));
+  FH_TRY(head<WT>(s, B));
   if (p.with_sample) LAUNCH(launch_sample(st, make_sample_args(s, p)));
   return FH_OK;
 }
@@ -426,7 +444,7 @@ int enqueue_decode_step(fh_session* s, const StepPlan& p) {
     FH_TRY(enqueue_layers_decode<WT>(s, src));
     const size_t lf = s->idx_lnf();
     LAUNCH(launch_layernorm(st, s->x, B, 1, 1, 0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
-    LAUNCH(launch_head<WT>(st, s->xn, B, D, s->w<WT>(s->idx_tok()), s->d.vocab_size, s->logits));
+    FH_TRY(head<WT>(s, B));
   }
   LAUNCH(launch_sample(st, make_sample_args(s, p)));
   return FH_OK;

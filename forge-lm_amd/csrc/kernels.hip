@@ -797,6 +797,13 @@ hipError_t launch_attn_decode(hipStream_t st, RowSrc src, const float* qkv, int 
   return hipGetLastError();
 }
 
+hipError_t launch_attn_decode_combine(hipStream_t st, RowSrc src, int B, int d, int H, int ctx, const float* part,
+                                      int chunk, int maxc, float* o) {
+  FH_CHECK_ARG(B > 0 && H > 0 && d % H == 0 && d / H <= 128 && chunk > 0 && maxc > 0 && part && o);
+  hipLaunchKernelGGL(k_attn_decode_combine, dim3(H, B), dim3(64), 0, st, src, d, H, ctx, part, chunk, maxc, o);
+  return hipGetLastError();
+}
+
 template <typename WT>
 hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* E, int V, float* logits) {
   constexpr int VEC = 16 / sizeof(WT);

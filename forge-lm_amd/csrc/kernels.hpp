@@ -55,6 +55,17 @@ template <typename KT>
 hipError_t launch_attn_decode(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
                               const KT* kcache, const KT* vcache, float* part, int chunk, float* o);
 
+// Combines the chunk partials part[(b*H + h)*maxc + c][hd + 2] (o, max, sum) of
+// the keys 0..pos (pos from src) into o[b, h*hd:].
+hipError_t launch_attn_decode_combine(hipStream_t st, RowSrc src, int B, int d, int H, int ctx, const float* part,
+                                      int chunk, int maxc, float* o);
+
+// The same decode attention for head_dim 64 (attn_decode.hip): 256-key chunks,
+// one 1 KB request per 4 K or V rows.  part must hold B*H*ceil(ctx/256)*66 floats.
+template <typename KT>
+hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
+                                   const KT* kcache, const KT* vcache, float* part, float* o);
+
 // Tied head for B rows: logits[b, v] = dot(xn[b,:], E[v,:]).
 template <typename WT>
 hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* E, int V, float* logits);

@@ -328,3 +328,19 @@ def test_head_dim_64_window_prefill_matches_oracle(fhp, oracle, backend, dtype):
                 break
             assert ids[b][n] == rids[n], (b, n)
     m.dispose()
+
+
+def test_batched_decode_attention_over_several_chunks(fhp, oracle, backend):
+    # batched decode attention reads 256-key chunks: a 500-token prompt decoded
+    # to position 529 crosses the second chunk boundary with a ragged last chunk
+    shape = (512, 640, 128, 2, 2)
+    B, P, NEW = 3, 500, 30
+    m, oc, w = make_model(fhp, oracle, backend, shape, 31, batch=B)
+    r = fhp.TrainingRandom(11)
+    prompts = np.stack([r.ids(shape[0], P) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
+    for b in range(B):
+        rids, rlg = oracle.generate(oc, w, prompts[b], NEW, return_logits=True)
+        np.testing.assert_array_equal(ids[b], rids)
+        assert rel_err(lg[b], rlg) <= TOL_F32
+    m.dispose()
