@@ -1,10 +1,11 @@
-"""Decode benchmark of the HIP token loop (BASELINE.json metric, config 2).
+"""Decode benchmark of the HIP token loop (BASELINE.json metric).
 
-One "step" = one Sampler.Generate pass over one batch: Forge-98M shape
-(12 layers, d 768, 12 heads, ctx 1024, V 16384), fp32, batch 1, a 64-token
-PCG32(42) prompt, 256 greedy tokens with the KV cache, random-init weights
-(new Random(1234), GptModel init).  Inputs are resident on the device before
-the timed region; only the 256 ids come back per step.
+Default workload (config 2, the headline): one "step" = one Sampler.Generate
+pass over one batch: Forge-98M shape (12 layers, d 768, 12 heads, ctx 1024,
+V 16384), fp32, batch 1, a 64-token PCG32(42) prompt, 256 greedy tokens with
+the KV cache, random-init weights (new Random(1234), GptModel init).  Inputs
+are resident on the device before the timed region; only the ids come back
+per step.
 
 value = generated tokens / wall time of the K timed steps (prefill included).
 roofline: the decode kernel's algorithmic HBM bytes per launch (per token:
@@ -15,7 +16,17 @@ cpu_baseline: the oracle's restatement of the reference CPU algorithm
 (full-window recompute per token, Sampler.Generate semantics) on this host,
 on the first tokens of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+The other configurations are separate lines, one per run:
+  --workload c3  sampling path (T 0.7, top-k 30, penalty 1.1, no-repeat 4-gram),
+                 prompt 32 + 512 tokens; roofline over one decode step
+  --workload c4  batch 32, prompts 512 (PCG32 seeds 42 + b) + 512 greedy;
+                 roofline over one batched decode step (weights + 32 KV windows)
+  --workload c5  Forge-220M shape, bf16 weights/activations, fp32 accumulation,
+                 batch 8 x 1024-token prompts + 128 greedy (every step
+                 re-prefills the full window); value = prefill tok/s, roofline
+                 = prefill FLOPs / prefill time against the bf16 MFMA peak
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload c2|c3|c4|c5]
 """
 from __future__ import annotations
 
@@ -29,9 +40,27 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "forge-lm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 C2 = dict(vocab_size=16384, context_length=1024, d_model=768, n_layers=12, n_heads=12)
+C5 = dict(vocab_size=16384, context_length=1024, d_model=1024, n_layers=16, n_heads=16)
+DIMS = ("vocab_size", "context_length", "d_model", "n_layers", "n_heads")
 PROMPT_LEN, NEW_TOKENS = 64, 256
+
+# name -> shape, dtype, batch, prompt length, new tokens, sampling (T, k, penalty, ngram, rng seed)
+WORKLOADS = {
+    "c2": dict(shape=C2, dtype="f32", batch=1, prompt=PROMPT_LEN, new=NEW_TOKENS, sampling=None,
+               desc="C2: Forge-98M shape (L12 d768 H12 ctx1024 V16384) fp32, batch 1, prompt 64 + 256 greedy, "
+                    "KV cache"),
+    "c3": dict(shape=C2, dtype="f32", batch=1, prompt=32, new=512, sampling=(0.7, 30, 1.1, 4, 1),
+               desc="C3: Forge-98M shape fp32, batch 1, prompt 32 + 512 sampled (T 0.7, top-k 30, repetition "
+                    "penalty 1.1, no-repeat-ngram 4, Random(1) uniforms), KV cache"),
+    "c4": dict(shape=C2, dtype="f32", batch=32, prompt=512, new=512, sampling=None,
+               desc="C4: Forge-98M shape fp32, batch 32, prompts 512 + 512 greedy, KV cache (windows 513..1023)"),
+    "c5": dict(shape=C5, dtype="bf16", batch=8, prompt=1024, new=128, sampling=None,
+               desc="C5: Forge-220M shape (L16 d1024 H16 ctx1024 V16384) bf16 weights and activations, fp32 "
+                    "accumulation, batch 8, prompts 1024 + 128 greedy (every step re-prefills the window)"),
+}
 
 
 def decode_bytes_per_step(c, attended: float, batch: int = 1, esize: int = 4) -> float:
@@ -42,23 +71,61 @@ def decode_bytes_per_step(c, attended: float, batch: int = 1, esize: int = 4) ->
     return weights + batch * per_seq
 
 
-def cpu_baseline(weights_seed: int, prompt, gpu_ids, budget_tokens: int = 96):
+def prefill_flops(c, T: int, batch: int) -> float:
+    """Algorithmic FLOPs of one prefill forward: the linear layers, causal QK^T and PV, the last-row head."""
+    d, L, V = c["d_model"], c["n_layers"], c["vocab_size"]
+    return batch * (2.0 * T * L * 12 * d * d + 2.0 * L * d * T * (T + 1) + 2.0 * V * d)
+
+
+def prompts_for(name: str, w: dict, vocab: int):
+    import numpy as np
+    import forge_hip as fhp
+    if w["batch"] == 1:
+        return fhp.TrainingRandom(42).ids(vocab, w["prompt"])
+    return np.stack([fhp.TrainingRandom(42 + b).ids(vocab, w["prompt"]) for b in range(w["batch"])])
+
+
+def bf16_round(x):
+    """fp32 -> nearest-even bf16 -> fp32 (what a bf16 session stores)."""
+    import numpy as np
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32)
+
+
+def cpu_baseline(name: str, w: dict, prompts, gpu_ids, budget_tokens: int):
+    """The oracle (reference CPU algorithm, full-window recompute) on a bounded sample of the workload."""
+    import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
     threads = min(16, os.cpu_count() or 1)
     O.set_threads(threads)
-    oc = O.Config(*[C2[k] for k in ("vocab_size", "context_length", "d_model", "n_layers", "n_heads")])
-    w = O.init_weights(oc, weights_seed)
+    oc = O.Config(*[w["shape"][k] for k in DIMS])
+    wt = O.init_weights(oc, 1234)
+    if w["dtype"] == "bf16":
+        wt = bf16_round(wt)
+    prompt = prompts if prompts.ndim == 1 else prompts[0]
+    gpu0 = gpu_ids if w["batch"] == 1 else gpu_ids[0]
+    n = min(budget_tokens, w["new"])
+    kw = {}
+    if w["sampling"]:
+        T, k, pen, ng, seed = w["sampling"]
+        kw = dict(temperature=T, top_k=k, uniforms=O.net_random_doubles(seed, n), penalty=pen, ngram=ng)
     t0 = time.perf_counter()
-    ids = O.generate(oc, w, prompt, budget_tokens, kv_cached=False)
+    ids = O.generate(oc, wt, prompt, n, kv_cached=False, **kw)
     dt = time.perf_counter() - t0
-    return {
-        "value": budget_tokens / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+    what = "sequence 0 of %d, " % w["batch"] if w["batch"] > 1 else ""
+    out = {
+        "value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
         "sample": (f"reference CPU algorithm (C++ restatement, full-window recompute per token as "
-                   f"Sampler.Generate does) on the C2 weights and prompt: first {budget_tokens} of "
-                   f"{NEW_TOKENS} tokens, {dt:.1f} s, {threads} threads"),
-        "ids_match_gpu": bool((ids == gpu_ids[:budget_tokens]).all()),
+                   f"Sampler.Generate does) on the {name.upper()} weights and prompt: {what}first {n} of "
+                   f"{w['new']} tokens, {dt:.1f} s, {threads} threads"),
+        "ids_match_gpu": bool((np.asarray(ids) == np.asarray(gpu0)[:n]).all()),
     }
+    if name == "c5":
+        # every C5 token is a full 1024-token window forward: also quote it as window tokens/s
+        out["window_tok_s"] = n * w["prompt"] / dt
+    return out
 
 
 def copy_calibration(mib: int, reps: int) -> dict:
@@ -92,14 +159,120 @@ def profiled_traffic(kernel: str):
     return None
 
 
+def run_workload(name: str, args) -> dict:
+    import numpy as np
+    import forge_hip as fhp
+
+    w = dict(WORKLOADS[name])
+    if args.new:
+        w["new"] = args.new
+        w["desc"] += f" (shortened to {args.new} new tokens)"
+    c = w["shape"]
+    cfg = fhp.ModelConfig(**c)
+    be = fhp.HipBackend(0)
+    model = fhp.GptModel(cfg, be, seed=1234, batch=w["batch"], dtype=w["dtype"])
+    prompts = prompts_for(name, w, cfg.vocab_size)
+    B, P, NEW = w["batch"], w["prompt"], w["new"]
+
+    def one():
+        if w["sampling"]:
+            T, k, pen, ng, seed = w["sampling"]
+            return fhp.Sampler.generate(model, prompts, NEW, T, k, fhp.Random(seed), None, pen, ng)
+        return fhp.Sampler.generate(model, prompts, NEW, 0.0, 0, None)
+
+    for _ in range(args.warmup):
+        ids = one()
+    decode_ms, prefill_ms, timings = [], [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ids = one()
+        t = fhp.Sampler.last_timing
+        timings.append(t)
+        decode_ms.append(t["decode_ms"])
+        prefill_ms.append(t["prefill_ms"])
+    wall = time.perf_counter() - t0
+    n_out = len(ids) if B == 1 else sum(len(r) for r in ids)
+    assert n_out == B * NEW, (n_out, B * NEW)
+
+    n_dec = NEW - 1  # step 0 comes from the prefill forward
+    dec_s = float(np.mean(decode_ms)) / 1e3
+    pre_s = float(np.mean(prefill_ms)) / 1e3
+    if n_dec == 0 and name != "c5":
+        raise SystemExit("--new must be at least 2 for a decode workload (token 0 comes from the prefill)")
+    avg_step_s = dec_s / n_dec if n_dec else 0.0
+    ctx = c["context_length"]
+    value = args.steps * B * NEW / wall
+    out = {
+        "metric": None, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
+        "data": "synthetic (random-init weights from new Random(1234); PCG32 prompt ids, seed 42 + sequence)",
+        "config": {"workload": w["desc"], "batch": B, "prompt_len": P, "new_tokens": NEW},
+    }
+    if name == "c5":
+        flops = prefill_flops(c, min(P, ctx), B)
+        tflops = flops / pre_s / 1e12
+        pre_tok = B * min(P, ctx) / pre_s
+        out.update({
+            "metric": "prefill tok/s, Forge-220M shape bf16 bs8 x 1024-token prompts",
+            "value": round(pre_tok, 1),
+            "ms_per_step": round(pre_s * 1e3, 3),
+            "decode_tok_s_reprefill": round(B * n_dec / dec_s, 1) if n_dec else None,
+            "reprefill_ms_per_step": round(avg_step_s * 1e3, 3),
+            "whole_job_tok_s": round(value, 2),
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "kernel": "prefill forward (GEMM, attention, LayerNorm, head kernels)",
+                         "flops_per_launch": flops, "launch_us": round(pre_s * 1e6, 1)},
+        })
+        # the timed unit is one prefill forward; value is its token rate
+        out["steps"] = args.steps
+    else:
+        # decode step n attends P+n keys (positions 0..P+n-1 plus itself), n = 1..NEW-1
+        attended = float(np.mean([min(P + n, ctx) for n in range(1, NEW)]))
+        step_bytes = decode_bytes_per_step(c, attended, batch=B)
+        achieved = step_bytes / avg_step_s / 1e9
+        fused = name == "c2" and os.environ.get("FORGE_HIP_FUSED_DECODE", "1") != "0"
+        kernel = "k_decode_step<768>" if fused else "decode step graph (generic kernels)"
+        tokens_per_launch = n_dec if fused else 1
+        out.update({
+            "decode_tok_s": round(B * n_dec / dec_s, 2),
+            "decode_us_per_step": round(avg_step_s * 1e6, 2),
+            "prefill_tok_s": round(B * P / pre_s, 2),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": profiled_traffic(kernel) if fused else None,
+                         "kernel": kernel, "tokens_per_launch": tokens_per_launch,
+                         "bytes_per_launch": int(step_bytes * tokens_per_launch),
+                         "launch_us": round(avg_step_s * tokens_per_launch * 1e6, 2)},
+        })
+        if name == "c2":
+            out["metric"] = "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)"
+            out["decode_us_per_token"] = out.pop("decode_us_per_step")
+        elif name == "c3":
+            out["metric"] = "decode tok/s, Forge-98M shape fp32 bs1 sampled (prompt 32 + 512)"
+        else:
+            out["metric"] = "decode tok/s, Forge-98M shape fp32 bs32 (prompt 512 + 512 greedy)"
+    out["device"] = be.device_name
+    if not args.no_cpu:
+        budget = args.cpu_tokens if args.cpu_tokens else {"c2": 96, "c3": 96, "c4": 12, "c5": 2}[name]
+        out["cpu_baseline"] = cpu_baseline(name, w, prompts, ids, budget)
+    model.dispose()
+    be.dispose()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--new", type=int, default=0,
+                    help="generate this many tokens instead of the workload's count (short profiling runs)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=96,
-                    help="tokens of the workload the CPU baseline runs (about 15-25 s on 16 cores)")
+    ap.add_argument("--cpu-tokens", type=int, default=0,
+                    help="tokens of the workload the CPU baseline runs (default: about 10-25 s on 16 cores)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only time the plain copy kernel on MIB MiB and print its line")
     args = ap.parse_args()
@@ -111,71 +284,7 @@ def main():
     if args.copy_calibration:
         print(json.dumps(copy_calibration(args.copy_calibration, max(1, args.steps))), flush=True)
         return
-
-    import numpy as np
-    import forge_hip as fhp
-
-    cfg = fhp.ModelConfig(**C2)
-    be = fhp.HipBackend(0)
-    model = fhp.GptModel(cfg, be, seed=1234)
-    prompt = fhp.TrainingRandom(42).ids(cfg.vocab_size, PROMPT_LEN)
-
-    for _ in range(args.warmup):
-        ids = fhp.Sampler.generate(model, prompt, NEW_TOKENS, 0.0, 0, None)
-    decode_ms, prefill_ms = [], []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ids = fhp.Sampler.generate(model, prompt, NEW_TOKENS, 0.0, 0, None)
-        t = fhp.Sampler.last_timing
-        decode_ms.append(t["decode_ms"])
-        prefill_ms.append(t["prefill_ms"])
-    wall = time.perf_counter() - t0
-    assert len(ids) == NEW_TOKENS
-
-    n_dec = NEW_TOKENS - 1  # step 0 comes from the prefill forward
-    avg_step_s = float(np.mean(decode_ms)) / 1e3 / n_dec
-    # decode step n attends positions 0..P+n-1 (P+n keys)
-    attended = np.mean([PROMPT_LEN + n for n in range(1, NEW_TOKENS)])
-    step_bytes = decode_bytes_per_step(C2, attended)
-    achieved = step_bytes / avg_step_s / 1e9
-    value = args.steps * NEW_TOKENS / wall
-    fused = os.environ.get("FORGE_HIP_FUSED_DECODE", "1") != "0"
-    kernel = "k_decode_step<768>" if fused else "decode step graph (generic kernels)"
-    # the fused greedy path runs every cached step in one launch; the generic
-    # path launches one graph per step
-    tokens_per_launch = n_dec if fused else 1
-    out = {
-        "metric": "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)",
-        "value": round(value, 2),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall / args.steps * 1e3, 3),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (random-init weights from new Random(1234); PCG32(42) prompt ids)",
-        "config": {"workload": "C2: Forge-98M shape (L12 d768 H12 ctx1024 V16384) fp32, batch 1, "
-                               "prompt 64 + 256 greedy, KV cache", "batch": 1, "prompt_len": PROMPT_LEN,
-                   "new_tokens": NEW_TOKENS},
-        "decode_tok_s": round(n_dec / (float(np.mean(decode_ms)) / 1e3), 2),
-        "decode_us_per_token": round(avg_step_s * 1e6, 2),
-        "prefill_tok_s": round(PROMPT_LEN / (float(np.mean(prefill_ms)) / 1e3), 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": profiled_traffic(kernel) if fused else None,
-                     "kernel": kernel, "tokens_per_launch": tokens_per_launch,
-                     "bytes_per_launch": int(step_bytes * tokens_per_launch),
-                     "launch_us": round(avg_step_s * tokens_per_launch * 1e6, 2)},
-        "device": be.device_name,
-    }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(1234, prompt, ids, args.cpu_tokens)
-    model.dispose()
-    be.dispose()
-    print(json.dumps(out), flush=True)
+    print(json.dumps(run_workload(args.workload, args)), flush=True)
 
 
 if __name__ == "__main__":

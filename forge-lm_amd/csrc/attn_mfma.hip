@@ -34,10 +34,10 @@ __device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + 
 
 __device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16(f)); }
 
-template <typename KT>
-__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restrict__ qkv, int T, int d, int H, int ctx,
-                                                          const KT* __restrict__ kc, const KT* __restrict__ vc,
-                                                          float* __restrict__ o) {
+template <typename KT, typename OT, typename QT>
+__global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict__ qp, int qstride, int T, int d, int H,
+                                                          int ctx, const KT* __restrict__ kc,
+                                                          const KT* __restrict__ vc, OT* __restrict__ o) {
   constexpr bool BF = sizeof(KT) == 2;
   // K tile [key][dim] and V^T tile [dim][key]; fp32 K rows hold the even dims
   // first, then the odd ones (float4 reads per half-wave)
@@ -55,10 +55,14 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
   const KT* V = vc + ((size_t)b * H + h) * ctx * HD;
 
   // this lane's q (row q, clamped for the loads)
-  const float* qrow = qkv + (size_t)(b * T + min(q, T - 1)) * 3 * d + h * HD;
+  const QT* qrow = qp + (size_t)(b * T + min(q, T - 1)) * qstride + h * HD;
   bf16x8_t qb[4];                          // bf16: dims 16kk + 8*half .. +7
   float qf[32];                            // fp32: dims 2s + half
-  if constexpr (BF) {
+  if constexpr (sizeof(QT) == 2) {
+    static_assert(BF, "bf16 q goes with a bf16 cache");
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) qb[kk] = *reinterpret_cast<const bf16x8_t*>(qrow + 16 * kk + 8 * half);
+  } else if constexpr (BF) {
 #pragma unroll
     for (int kk = 0; kk < 4; kk++) {
       const float4 a = *reinterpret_cast<const float4*>(qrow + 16 * kk + 8 * half);
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
 
   if (q >= T) return;
   const float inv = 1.f / l;
-  float* orow = o + (size_t)(b * T + q) * d + h * HD;
+  OT* orow = o + (size_t)(b * T + q) * d + h * HD;
 #pragma unroll
   for (int dt = 0; dt < 2; dt++)
 #pragma unroll
@@ -221,25 +225,42 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const float* __restri
       // elements 4g .. 4g+3 are dims dt*32 + 8g + 4*half + 0..3
       const float4 v = make_float4(ot[dt][4 * g] * inv, ot[dt][4 * g + 1] * inv, ot[dt][4 * g + 2] * inv,
                                    ot[dt][4 * g + 3] * inv);
-      *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * half) = v;
+      if constexpr (sizeof(OT) == 2) {
+        const uint32_t lo = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+        *reinterpret_cast<uint2*>(orow + dt * 32 + 8 * g + 4 * half) = make_uint2(lo, hi);
+      } else {
+        *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * half) = v;
+      }
     }
 }
 
 }  // namespace
 
-template <typename KT>
+template <typename KT, typename OT>
 hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
-                                    const KT* kcache, const KT* vcache, float* o) {
+                                    const KT* kcache, const KT* vcache, OT* o) {
   if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !qkv || !kcache || !vcache || !o)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_prefill_mfma<KT>, dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, qkv, T, d, H, ctx,
-                     kcache, vcache, o);
+  hipLaunchKernelGGL((k_attn_prefill_mfma<KT, OT, float>), dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, qkv,
+                     3 * d, T, d, H, ctx, kcache, vcache, o);
   return hipGetLastError();
 }
 
-template hipError_t launch_attn_prefill_mfma<float>(hipStream_t, const float*, int, int, int, int, int, const float*,
-                                                    const float*, float*);
-template hipError_t launch_attn_prefill_mfma<bf16_t>(hipStream_t, const float*, int, int, int, int, int,
-                                                     const bf16_t*, const bf16_t*, float*);
+hipError_t launch_attn_prefill_mfma_q16(hipStream_t st, const bf16_t* q, int B, int T, int d, int H, int ctx,
+                                        const bf16_t* kcache, const bf16_t* vcache, bf16_t* o) {
+  if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !q || !kcache || !vcache || !o)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_attn_prefill_mfma<bf16_t, bf16_t, bf16_t>), dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st,
+                     q, d, T, d, H, ctx, kcache, vcache, o);
+  return hipGetLastError();
+}
+
+template hipError_t launch_attn_prefill_mfma<float, float>(hipStream_t, const float*, int, int, int, int, int,
+                                                           const float*, const float*, float*);
+template hipError_t launch_attn_prefill_mfma<bf16_t, float>(hipStream_t, const float*, int, int, int, int, int,
+                                                            const bf16_t*, const bf16_t*, float*);
+template hipError_t launch_attn_prefill_mfma<bf16_t, bf16_t>(hipStream_t, const float*, int, int, int, int, int,
+                                                             const bf16_t*, const bf16_t*, bf16_t*);
 
 }  // namespace fh

@@ -197,6 +197,7 @@ struct fh_session {
   // fast decode path state
   FastDecode fast;
   bool fast_allowed = true;  // FORGE_HIP_FUSED_DECODE=0 at session creation selects the generic kernels
+  bool bf16_act = true;      // FORGE_HIP_BF16_ACT=0 keeps a bf16 session's window GEMMs on fp32 operands
   bool counted = false;      // holds a reference on its context
   bool use_fast() const { return fast.enabled && fast_allowed; }
   // graphs
@@ -302,10 +303,44 @@ int head(fh_session* s, int B) {
   return FH_OK;
 }
 
+// bf16 sessions over many rows: the GEMM operands (LayerNorm, attention and GELU
+// outputs) are written in bf16, rounded as the fp32-operand GEMM rounds them, into
+// the same buffers (xn, o, h hold M*D, M*D, M*4D floats, twice the bf16 bytes).
+// The QKV GEMM writes q in bf16 (as the attention kernel rounds it) and K, V
+// straight into the bf16 caches.
+int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T;
+  bf16_t* xnh = reinterpret_cast<bf16_t*>(s->xn);
+  bf16_t* oh = reinterpret_cast<bf16_t*>(s->o);
+  bf16_t* hh = reinterpret_cast<bf16_t*>(s->h);
+  bf16_t* qh = reinterpret_cast<bf16_t*>(s->qkv);  // q [M][D] in bf16 (the fp32 qkv rows are not written)
+  for (int l = 0; l < s->d.n_layers; l++) {
+    bf16_t* kc = reinterpret_cast<bf16_t*>(s->kc) + (size_t)l * s->kv_layer;
+    bf16_t* vc = reinterpret_cast<bf16_t*>(s->vc) + (size_t)l * s->kv_layer;
+    LAUNCH(launch_layernorm_bf16(st, s->x, M, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), xnh, D, 1e-5f));
+    LAUNCH(launch_gemm_bf16_qkv(st, xnh, M, D, s->wt<bf16_t>(s->idx_blk(l, 2)), s->v(s->idx_blk(l, 3)), src, T, H, C,
+                                qh, kc, vc));
+    LAUNCH(launch_attn_prefill_mfma_q16(st, qh, B, T, D, H, C, kc, vc, oh));
+    LAUNCH(launch_gemm_bf16(st, oh, M, D, s->wt<bf16_t>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x,
+                            s->x2, nullptr));
+    LAUNCH(launch_layernorm_bf16(st, s->x2, M, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), xnh, D, 1e-5f));
+    LAUNCH(launch_gemm_bf16(st, xnh, M, D, s->wt<bf16_t>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU,
+                            nullptr, nullptr, hh));
+    LAUNCH(launch_gemm_bf16(st, hh, M, 4 * D, s->wt<bf16_t>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)),
+                            EPI_RESIDUAL, s->x2, s->x, nullptr));
+  }
+  return FH_OK;
+}
+
 template <typename WT>
 int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
   hipStream_t st = s->ctx->stream;
   const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T;
+  if constexpr (sizeof(WT) == 2) {
+    if (s->bf16_act && M >= 256 && D % 64 == 0 && D == 64 * H)
+      return enqueue_layers_window_bf16(s, T, src);
+  }
   for (int l = 0; l < s->d.n_layers; l++) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
@@ -314,7 +349,7 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, T, D, H, C, kc, vc));
     if (D == 64 * H)
-      LAUNCH(launch_attn_prefill_mfma<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
+      LAUNCH((launch_attn_prefill_mfma<WT, float>(st, s->qkv, B, T, D, H, C, kc, vc, s->o)));
     else
       LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
     FH_TRY(linear<WT>(s, s->o, M, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x, s->x2));
@@ -692,12 +727,20 @@ int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_de
   const bool bf = dtype == FH_DTYPE_BF16;
   hipError_t e = hipSuccess;
   if (K % 32 == 0) {
-    // the GEMM takes the weights transposed, plus room for split-K partials
-    const size_t esz = bf ? 2 : 4, part_floats = (size_t)8 * M * N;
+    // the GEMM takes the weights transposed, plus room for split-K partials (or,
+    // for bf16 with many rows, for a rounded to bf16: the window path's kernel)
+    const bool big = bf && M >= 256 && K % 64 == 0;
+    const size_t esz = bf ? 2 : 4, part_floats = big ? 0 : (size_t)8 * M * N;
     char* tmp = nullptr;
-    HIP_TRY(hipMalloc(&tmp, (size_t)N * K * esz + part_floats * 4));
+    HIP_TRY(hipMalloc(&tmp, (size_t)N * K * esz + (big ? (size_t)M * K * 2 : part_floats * 4)));
     float* part = reinterpret_cast<float*>(tmp + (size_t)N * K * esz);
-    if (bf) {
+    if (big) {
+      bf16_t* wt = reinterpret_cast<bf16_t*>(tmp);
+      bf16_t* ah = wt + (size_t)N * K;
+      e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, wt);
+      if (e == hipSuccess) e = launch_round_bf16(st, a, (size_t)M * K, ah);
+      if (e == hipSuccess) e = launch_gemm_bf16(st, ah, M, K, wt, N, nullptr, EPI_NONE, res, y, nullptr);
+    } else if (bf) {
       e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, reinterpret_cast<bf16_t*>(tmp));
       if (e == hipSuccess)
         e = launch_gemm_mfma<bf16_t>(st, a, M, K, reinterpret_cast<const bf16_t*>(tmp), N, nullptr, EPI_NONE, res, y,
@@ -799,6 +842,8 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
   }
   const char* fused_env = getenv("FORGE_HIP_FUSED_DECODE");
   sp->fast_allowed = !(fused_env && fused_env[0] == '0');
+  const char* act_env = getenv("FORGE_HIP_BF16_ACT");
+  sp->bf16_act = !(act_env && act_env[0] == '0');
   if (sp->fast_allowed && (rc = sp->fast.init(*desc, c->props.multiProcessorCount)) != FH_OK)
     return fail(set_err(rc, "allocating the fused decode state failed"));
   c->sessions++;

@@ -19,6 +19,7 @@
 // bias (if any) and applies GELU / the residual.  With S == 1 the epilogue is
 // fused.
 #include "kernels.hpp"
+#include "mfma_epi.hpp"
 
 namespace fh {
 
@@ -29,10 +30,6 @@ constexpr int BK = 32;   // k per stage
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-
-// MFMA 32x32 accumulator layout: lane l holds column l % 32 and, in element r,
-// row (r / 4) * 8 + (l / 32) * 4 + r % 4.
-__device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
 template <typename WT>
 struct Tr;
@@ -51,10 +48,10 @@ struct Tr<float> {
   typedef float elem;
 };
 
-template <typename WT, int BM>
+template <typename WT, int BM, int EPI, bool RES>
 __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, int M, int K,
                                                   const WT* __restrict__ Wt, int N, int kchunk,
-                                                  const float* __restrict__ bias, int epi,
+                                                  const float* __restrict__ bias,
                                                   const float* __restrict__ res, float* __restrict__ Y,
                                                   float* __restrict__ part) {
   using E = typename Tr<WT>::elem;
@@ -167,23 +164,19 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
 
   const int col = n0 + w * 32 + fr;
   if (col >= N) return;
-  const float bcol = (part || !bias) ? 0.f : bias[col];
+  const int nrows = min(BM, M - m0);
+  if (part) {
+    // split-K partial of this block's K chunk: raw sums, no bias or epilogue
+    const __amdgpu_buffer_rsrc_t rp = rows_rsrc(part, (size_t)blockIdx.z * M + m0, nrows, N, 4);
 #pragma unroll
-  for (int t = 0; t < MT; t++) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = m0 + t * 32 + acc_row(lane, r);
-      if (row >= M) continue;
-      if (part) {
-        part[((size_t)blockIdx.z * M + row) * N + col] = acc[t][r];
-      } else {
-        float s = acc[t][r] + bcol;
-        if (epi == EPI_GELU) s = gelu_tanh(s);
-        if (res) s += res[(size_t)row * N + col];
-        Y[(size_t)row * N + col] = s;
-      }
-    }
+    for (int t = 0; t < MT; t++) mfma_store_tile<EPI_NONE, false, false>(acc[t], lane, t * 32, col, N, 0.f, rp, rp);
+    return;
   }
+  const float bcol = bias ? bias[col] : 0.f;
+  const __amdgpu_buffer_rsrc_t ry = rows_rsrc(Y, m0, nrows, N, 4);
+  const __amdgpu_buffer_rsrc_t rres = RES ? rows_rsrc(res, m0, nrows, N, 4) : ry;  // unused without RES
+#pragma unroll
+  for (int t = 0; t < MT; t++) mfma_store_tile<EPI, RES, false>(acc[t], lane, t * 32, col, N, bcol, rres, ry);
 }
 
 // Wt[n][k] = W[k][n] (one-time weight transpose at session load), 32x32 LDS tiles
@@ -208,6 +201,26 @@ hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt) {
   return hipGetLastError();
 }
 
+// the epilogue (GELU or not, residual or not) is a template parameter of the kernel
+template <typename WT, int BM>
+static hipError_t launch_epi(hipStream_t st, dim3 grid, const float* a, int M, int K, const WT* Wt, int N, int kchunk,
+                             const float* bias, int epi, const float* res, float* y, float* part) {
+  const bool gelu = epi == EPI_GELU;
+  if (part || (!gelu && !res))
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, false>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
+                       res, y, part);
+  else if (!gelu)
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, true>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
+                       res, y, part);
+  else if (!res)
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, false>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
+                       res, y, part);
+  else
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, true>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
+                       res, y, part);
+  return hipGetLastError();
+}
+
 template <typename WT>
 hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, const float* bias,
                             int epi, const float* res, float* y, float* part, size_t part_floats, int cus) {
@@ -223,13 +236,13 @@ hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const 
   const int kchunk = K / S;
   dim3 grid(gn, gm, S);
   float* pp = S > 1 ? part : nullptr;
+  hipError_t e;
   if (bm == 128)
-    hipLaunchKernelGGL((k_gemm_mfma<WT, 128>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+    e = launch_epi<WT, 128>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   else if (bm == 64)
-    hipLaunchKernelGGL((k_gemm_mfma<WT, 64>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+    e = launch_epi<WT, 64>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   else
-    hipLaunchKernelGGL((k_gemm_mfma<WT, 32>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
-  hipError_t e = hipGetLastError();
+    e = launch_epi<WT, 32>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   if (e != hipSuccess || S == 1) return e;
   return launch_splitk_epilogue(st, part, S, M, N, bias, epi, res, y);
 }

@@ -89,9 +89,10 @@ __global__ __launch_bounds__(256) void k_embed(RowSrc src, int T, const WT* __re
 // ---------------------------------------------------------------------------
 // LayerNorm, one 256-thread block per row
 // ---------------------------------------------------------------------------
+template <typename OT>
 __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ in, int rows_per_seq,
                                                    int seq_stride, int r_in0, const float* __restrict__ w,
-                                                   const float* __restrict__ b, float* __restrict__ out, int d,
+                                                   const float* __restrict__ b, OT* __restrict__ out, int d,
                                                    float eps) {
   __shared__ float red[4];
   const int r = blockIdx.x;
@@ -107,7 +108,48 @@ __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ in,
   }
   const float var = block_sum<256>(v, red);
   const float rs = 1.f / sqrtf(var / (float)d + eps);
-  for (int c = threadIdx.x; c < d; c += 256) out[(size_t)r * d + c] = (xr[c] - mu) * rs * w[c] + b[c];
+  for (int c = threadIdx.x; c < d; c += 256) out[(size_t)r * d + c] = from_f32<OT>((xr[c] - mu) * rs * w[c] + b[c]);
+}
+
+// The same for d a multiple of 256, one wave per row, rounded to bf16: the row
+// stays in registers (VPL float4 per lane, coalesced 1 KB loads), mean and
+// variance are wave sums, the output goes out as 8-byte bf16 quads.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __restrict__ in, int rows,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ b, bf16_t* __restrict__ out,
+                                                             float eps) {
+  constexpr int d = 256 * VPL;
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const float4* xr = reinterpret_cast<const float4*>(in + (size_t)r * d);
+  float4 x[VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    x[i] = xr[i * 64 + lane];
+    s += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+  }
+  const float mu = wave_sum_dpp(s) / (float)d;
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    x[i] = make_float4(x[i].x - mu, x[i].y - mu, x[i].z - mu, x[i].w - mu);
+    v += (x[i].x * x[i].x + x[i].y * x[i].y) + (x[i].z * x[i].z + x[i].w * x[i].w);
+  }
+  const float rs = 1.f / sqrtf(wave_sum_dpp(v) / (float)d + eps);
+  uint2* orow = reinterpret_cast<uint2*>(out + (size_t)r * d);
+#pragma unroll
+  for (int i = 0; i < VPL; i++) {
+    const float4 wv = reinterpret_cast<const float4*>(w)[i * 64 + lane];
+    const float4 bv = reinterpret_cast<const float4*>(b)[i * 64 + lane];
+    const uint32_t lo = (uint32_t)f32_to_bf16(x[i].x * rs * wv.x + bv.x) |
+                        ((uint32_t)f32_to_bf16(x[i].y * rs * wv.y + bv.y) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16(x[i].z * rs * wv.z + bv.z) |
+                        ((uint32_t)f32_to_bf16(x[i].w * rs * wv.w + bv.w) << 16);
+    orow[i * 64 + lane] = make_uint2(lo, hi);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -707,6 +749,12 @@ __global__ void k_copy_bytes(const uint4* __restrict__ src, uint4* __restrict__ 
   if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
 
+// out[i] = bf16(in[i]), nearest-even, over a grid-stride loop
+__global__ void k_round_bf16(const float* __restrict__ in, bf16_t* __restrict__ out, size_t n) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = f32_to_bf16(in[i]);
+}
+
 // ---------------------------------------------------------------------------
 // launch wrappers
 // ---------------------------------------------------------------------------
@@ -726,8 +774,25 @@ hipError_t launch_embed(hipStream_t st, RowSrc src, int B, int T, const WT* tok,
 hipError_t launch_layernorm(hipStream_t st, const float* in, int rows, int rows_per_seq, int seq_stride, int r_in0,
                             const float* w, const float* b, float* out, int d, float eps) {
   FH_CHECK_ARG(rows > 0 && rows_per_seq > 0 && d > 0 && in && w && b && out);
-  hipLaunchKernelGGL(k_layernorm, dim3(rows), dim3(256), 0, st, in, rows_per_seq, seq_stride, r_in0, w, b, out, d,
-                     eps);
+  hipLaunchKernelGGL(k_layernorm<float>, dim3(rows), dim3(256), 0, st, in, rows_per_seq, seq_stride, r_in0, w, b, out,
+                     d, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_layernorm_bf16(hipStream_t st, const float* in, int rows, const float* w, const float* b,
+                                 bf16_t* out, int d, float eps) {
+  FH_CHECK_ARG(rows > 0 && d > 0 && in && w && b && out);
+  const dim3 g((rows + 3) / 4);
+  if (d == 1024)
+    hipLaunchKernelGGL(k_layernorm_rows_bf16<4>, g, dim3(256), 0, st, in, rows, w, b, out, eps);
+  else if (d == 768)
+    hipLaunchKernelGGL(k_layernorm_rows_bf16<3>, g, dim3(256), 0, st, in, rows, w, b, out, eps);
+  else if (d == 512)
+    hipLaunchKernelGGL(k_layernorm_rows_bf16<2>, g, dim3(256), 0, st, in, rows, w, b, out, eps);
+  else if (d == 256)
+    hipLaunchKernelGGL(k_layernorm_rows_bf16<1>, g, dim3(256), 0, st, in, rows, w, b, out, eps);
+  else
+    hipLaunchKernelGGL(k_layernorm<bf16_t>, dim3(rows), dim3(256), 0, st, in, rows, 0, 0, w, b, out, d, eps);
   return hipGetLastError();
 }
 
@@ -810,6 +875,15 @@ hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* 
   FH_CHECK_ARG(B > 0 && d > 0 && d <= 1024 && d % VEC == 0 && V > 0 && xn && E && logits);
   const int blocks = min(1024, (V + 3) / 4);
   hipLaunchKernelGGL(k_head<WT>, dim3(blocks), dim3(256), 0, st, xn, B, d, E, V, logits);
+  return hipGetLastError();
+}
+
+hipError_t launch_round_bf16(hipStream_t st, const float* in, size_t n, bf16_t* out) {
+  FH_CHECK_ARG(in && out);
+  if (n == 0) return hipSuccess;
+  const size_t want = (n + 255) / 256;
+  const unsigned blocks = (unsigned)(want < 8192 ? want : 8192);
+  hipLaunchKernelGGL(k_round_bf16, dim3(blocks), dim3(256), 0, st, in, out, n);
   return hipGetLastError();
 }
 

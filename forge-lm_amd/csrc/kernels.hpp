@@ -8,7 +8,7 @@
 
 namespace fh {
 
-enum Epilogue : int { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2 };
+enum Epilogue : int { EPI_NONE = 0, EPI_GELU = 1, EPI_RESIDUAL = 2, EPI_QKV = 3 };
 
 // x[r,:] = tok_emb[id(r)] + pos_emb[pos(r)] for rows r = b*T + t.
 template <typename WT>
@@ -18,6 +18,10 @@ hipError_t launch_embed(hipStream_t st, RowSrc src, int B, int T, const WT* tok,
 // out[r,:] = LN(in[r_in,:]) with r_in = r_in0 + (r / rows_per_seq) * seq_stride + (r % rows_per_seq).
 hipError_t launch_layernorm(hipStream_t st, const float* in, int rows, int rows_per_seq, int seq_stride,
                             int r_in0, const float* w, const float* b, float* out, int d, float eps);
+
+// The same for every row of in (rows_per_seq = rows), rounded to bf16 into out.
+hipError_t launch_layernorm_bf16(hipStream_t st, const float* in, int rows, const float* w, const float* b,
+                                 bf16_t* out, int d, float eps);
 
 // Split-K GEMV for M <= 4 rows: part[s][m][n] = sum_{k in chunk s} x[m,k] W[k,n].
 template <typename WT>
@@ -44,10 +48,15 @@ hipError_t launch_attn_prefill(hipStream_t st, const float* qkv, int B, int T, i
                                const KT* kcache, const KT* vcache, float* o);
 
 // The same on MFMA tiles (attn_mfma.hip), for head_dim 64: bf16 caches multiply in bf16
-// (q and the softmax weights rounded to bf16), fp32 caches in fp32.
-template <typename KT>
+// (q and the softmax weights rounded to bf16), fp32 caches in fp32.  o is fp32, or
+// bf16 (rounded) for a bf16 session's large-M GEMM.
+template <typename KT, typename OT>
 hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
-                                    const KT* kcache, const KT* vcache, float* o);
+                                    const KT* kcache, const KT* vcache, OT* o);
+
+// The same with q already in bf16, q [B*T][d] (from launch_gemm_bf16_qkv).
+hipError_t launch_attn_prefill_mfma_q16(hipStream_t st, const bf16_t* q, int B, int T, int d, int H, int ctx,
+                                        const bf16_t* kcache, const bf16_t* vcache, bf16_t* o);
 
 // Decode attention of one row per sequence over keys 0..pos (pos from src), split over
 // chunks of `chunk` keys, then combined.  part must hold B*H*max_chunks*(hd+2) floats.
@@ -77,9 +86,37 @@ template <typename WT>
 hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, const float* bias,
                             int epi, const float* res, float* y, float* part, size_t part_floats, int cus);
 
+// bf16 GEMM for large M (gemm_bf16.hip): y = epi(a[M,K] @ W + bias) (+ res) with a
+// in bf16 and W given transposed as Wt[N][K] bf16; K a multiple of 64.  Exactly one
+// of y (fp32) and yh (bf16, rounded) is the output.
+hipError_t launch_gemm_bf16(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
+                            const float* bias, int epi, const float* res, float* y, bf16_t* yh);
+
+// Outputs of the bf16 GEMM's epilogues (one set is used per launch).
+struct GemmBf16Out {
+  const float* res;  // residual added to y, or null
+  float* y;          // fp32 output [M][N]
+  bf16_t* yh;        // bf16 output [M][N]
+  bf16_t* q;         // EPI_QKV: q [M][D]; K and V into the caches [B][H][ctx][64] at pos(row)
+  bf16_t* kc;
+  bf16_t* vc;
+  RowSrc src;
+  int T, H, ctx;
+};
+
+// The QKV projection of a window with the cache store fused (replaces the fp32
+// qkv row + launch_kv_store): y = a @ Wqkv + b over M = B*T rows, q columns
+// rounded to bf16 into q [M][D], K and V columns into kcache / vcache at the
+// row's position (rows past ctx are dropped), D = 64 H.
+hipError_t launch_gemm_bf16_qkv(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, const float* bias,
+                                RowSrc src, int T, int H, int ctx, bf16_t* q, bf16_t* kcache, bf16_t* vcache);
+
 // Wt[n][k] = W[k][n].
 template <typename WT>
 hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt);
+
+// out[i] = in[i] rounded to bf16 (nearest-even), i < n.
+hipError_t launch_round_bf16(hipStream_t st, const float* in, size_t n, bf16_t* out);
 
 // dst[0..bytes) = src[0..bytes) on the device (both 16-byte aligned).
 hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);

@@ -255,6 +255,29 @@ def test_matmul_nn_matches_oracle(fhp, oracle, backend, M, K, N, dtype):
         buf.free()
 
 
+@pytest.mark.parametrize("M,K,N", [(2000, 512, 4000), (256, 4096, 1024), (8192, 1024, 256)])
+def test_matmul_nn_bf16_large_tiles(fhp, backend, M, K, N):
+    # bf16 products of 256 rows or more run on the bf16-operand GEMM of the window
+    # path: 256 x 128 tiles once there are as many tiles as CUs (the first and last
+    # cases, ragged in M and N in the first), 128 x 128 below that
+    r = np.random.default_rng(M + K + N)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    a_used, _ = bf16_round(a)
+    b_used, b_bits = bf16_round(b)
+    bufa = fhp.DeviceBuffer.from_array(backend, a)
+    bufb = fhp.DeviceBuffer.from_array(backend, b_bits)
+    bufy = fhp.DeviceBuffer.from_array(backend, y0)
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=True, dtype="bf16")
+    got = bufy.read(np.float32, M * N).reshape(M, N)
+    ref = y0.astype(np.float64) + a_used.astype(np.float64) @ b_used.astype(np.float64)
+    scale = np.abs(a_used).astype(np.float64) @ np.abs(b_used).astype(np.float64) + np.abs(y0)
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-6), float(np.max(np.abs(got - ref) / (scale + 1e-6)))
+    for buf in (bufa, bufb, bufy):
+        buf.free()
+
+
 def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
     # Forge-220M shape with bf16 weights, reduced to a 64-token
     # prompt and 3 steps per sequence so the CPU oracle stays quick; the oracle runs
@@ -280,6 +303,44 @@ def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
             else:
                 break
     m.dispose()
+
+
+@pytest.mark.parametrize("B,P", [(4, 64), (8, 1024)])
+def test_c5_shape_bf16_window_path_matches_oracle(fhp, oracle, backend, B, P):
+    # 256 window rows or more in a bf16 session: LayerNorm, attention and GELU write
+    # bf16 operands for the bf16 GEMM (B*P = 256 uses 128-row tiles, 8192 the
+    # 256-row tiles of the full C5 prefill; P = 1024 fills the window, so the second
+    # token re-prefills it).  Checked against the oracle on bf16-rounded parameters
+    # (2e-2) for the first and last sequence, and against the fp32-operand path
+    shape = (16384, 1024, 1024, 16, 16)
+    NEW = 2
+    ocfg = oracle.Config(*shape)
+    w = oracle.init_weights(ocfg, 1234)
+    wr = bf16_round(w)[0]
+    prompts = np.stack([fhp.TrainingRandom(42 + b).ids(shape[0], P) for b in range(B)])
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype="bf16")
+    m.load_weights(w)
+    ids, lg = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
+    m.dispose()
+    os.environ["FORGE_HIP_BF16_ACT"] = "0"
+    try:
+        m2 = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype="bf16")
+    finally:
+        del os.environ["FORGE_HIP_BF16_ACT"]
+    m2.load_weights(w)
+    ids2, lg2 = fhp.Sampler.generate(m2, prompts, NEW, 0.0, 0, None, return_logits=True)
+    m2.dispose()
+    oracle.set_threads(16)
+    for b in (0, B - 1):
+        # the two paths round the same operands to bf16 but sum in different orders
+        # (split K in the fp32-operand GEMM); 16 layers of bf16 rounding carry that
+        # to about 1e-2 of the logits, inside the bf16 bar
+        assert rel_err(lg[b][0], lg2[b][0]) <= 2e-2
+        rids, rlg = oracle.generate(ocfg, wr, prompts[b], NEW, return_logits=True)
+        assert rel_err(lg[b], rlg) <= 2e-2
+        top2 = np.sort(rlg[0])[-2:]
+        if top2[1] - top2[0] > 4e-2:
+            assert ids[b][0] == rids[0]
 
 
 def test_c4_shape_batched_decode_matches_oracle(fhp, oracle, backend):
