@@ -29,6 +29,7 @@ constexpr int BKV = 64;  // keys per tile
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
@@ -235,6 +236,182 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
     }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 sessions with q already in bf16: the same S^T / O^T scheme, software-
+// pipelined.  The K and V^T tiles of key tile j + 1 are fetched into registers
+// while tile j is multiplied and land in the other half of a double-buffered
+// LDS pair (one barrier per tile).  V^T is built in registers: a thread takes
+// one dim pair of 8 key rows (4-byte loads, a wave covers whole 128-byte rows)
+// and packs them with v_perm into two 16-byte rows of V^T.  Within each group
+// of 16 keys V^T holds the keys in the order the score registers hold them
+// (0-3, 8-11, 4-7, 12-15), so an A fragment is one 16-byte LDS read.  The
+// softmax runs in base 2 on the hardware exp (scores pre-scaled by
+// log2(e) / 8), the causal mask only on tiles that cross the wave's diagonal,
+// and P is rounded to bf16 by the hardware packed convert.  Rows at or past T
+// read as zeros (bounded buffer loads), so stale cache rows never meet a zero
+// weight.  The heaviest query blocks (latest queries) are dispatched first.
+// ---------------------------------------------------------------------------
+constexpr int KP = HD + 8;  // bf16 per LDS row of K (dims) and V^T (keys): 144 B, 16 rows hit distinct banks
+
+__global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __restrict__ qp, int T, int d, int H,
+                                                              int ctx, const bf16_t* __restrict__ kc,
+                                                              const bf16_t* __restrict__ vc, bf16_t* __restrict__ o) {
+  __shared__ __align__(16) __bf16 Ks[2][BKV][KP];
+  __shared__ __align__(16) __bf16 Vt[2][HD][KP];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t0 = (gridDim.x - 1 - blockIdx.x) * BQ, h = blockIdx.y, b = blockIdx.z;
+  const int qw0 = t0 + 32 * w;
+  const int q = qw0 + (lane & 31), half = lane >> 5;
+  const float sl2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
+  const size_t head = ((size_t)b * H + h) * ctx * HD;
+  // this (sequence, head)'s first T cache rows; rows past T read as zeros
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(kc + head), (short)0, T * HD * 2, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(vc + head), (short)0, T * HD * 2, 0x00020000);
+
+  const bf16_t* qrow = qp + (size_t)(b * T + min(q, T - 1)) * d + h * HD;
+  bf16x8_t qb[4];  // dims 16kk + 8*half .. +7
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++) qb[kk] = *reinterpret_cast<const bf16x8_t*>(qrow + 16 * kk + 8 * half);
+
+  // staging roles: K piece (key kp_key, 16 bytes at dim 8*kp_c) for i = 0, 1;
+  // V: dim pair vc2 of keys vkey(u), u = 0..7, to V^T positions vpos .. +7
+  const int kp_key = tid >> 3, kp_c = tid & 7;
+  const int vc2 = tid & 31, vkq = tid >> 5, vg = vkq >> 1, vsel = vkq & 1;
+  auto vkey = [&](int u) { return vg * 16 + vsel * 4 + (u >> 2) * 8 + (u & 3); };
+  const int vpos = vg * 16 + vsel * 8;
+  uint4 kr[2];
+  unsigned vr[8];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rk, ((k0 + kp_key + 32 * i) * HD + 8 * kp_c) * 2, 0, 0);
+      kr[i] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) vr[u] = __builtin_amdgcn_raw_buffer_load_b32(rv, ((k0 + vkey(u)) * HD + 2 * vc2) * 2, 0, 0);
+  };
+  auto put = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) *reinterpret_cast<uint4*>(&Ks[buf][kp_key + 32 * i][8 * kp_c]) = kr[i];
+    // V^T rows 2*vc2 (low halves) and 2*vc2 + 1 (high halves) of the 8 keys
+    const uint4 lo = make_uint4(__builtin_amdgcn_perm(vr[1], vr[0], 0x05040100u),
+                                __builtin_amdgcn_perm(vr[3], vr[2], 0x05040100u),
+                                __builtin_amdgcn_perm(vr[5], vr[4], 0x05040100u),
+                                __builtin_amdgcn_perm(vr[7], vr[6], 0x05040100u));
+    const uint4 hi = make_uint4(__builtin_amdgcn_perm(vr[1], vr[0], 0x07060302u),
+                                __builtin_amdgcn_perm(vr[3], vr[2], 0x07060302u),
+                                __builtin_amdgcn_perm(vr[5], vr[4], 0x07060302u),
+                                __builtin_amdgcn_perm(vr[7], vr[6], 0x07060302u));
+    *reinterpret_cast<uint4*>(&Vt[buf][2 * vc2][vpos]) = lo;
+    *reinterpret_cast<uint4*>(&Vt[buf][2 * vc2 + 1][vpos]) = hi;
+  };
+
+  f32x16_t ot[2];  // O^T: dims (dt*32 + acc_row) x this lane's query
+#pragma unroll
+  for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) ot[dt][r] = 0.f;
+  float m = -INFINITY, l = 0.f;  // running max (base-2 scaled) and sum
+
+  const int qlast = min(t0 + BQ, T) - 1;
+  const int nkt = qlast / BKV + 1;
+  fetch(0);
+  put(0);
+  __syncthreads();
+  for (int kt = 0; kt < nkt; kt++) {
+    const int k0 = kt * BKV, buf = kt & 1;
+    if (kt + 1 < nkt) fetch(k0 + BKV);
+    if (k0 <= qw0 + 31 && qw0 < T) {  // some query of this wave sees a key of the tile
+      f32x16_t s[2];
+#pragma unroll
+      for (int jt = 0; jt < 2; jt++) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) s[jt][r] = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(&Ks[buf][jt * 32 + (lane & 31)][16 * kk + 8 * half]);
+          s[jt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[kk], s[jt], 0, 0, 0);
+        }
+      }
+      float mt = -INFINITY;
+      if (k0 + BKV - 1 > qw0) {  // the tile crosses this wave's diagonal: mask keys past the query
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const int key = k0 + jt * 32 + acc_row(lane, r);
+            const float v = key <= q ? s[jt][r] * sl2 : -INFINITY;
+            s[jt][r] = v;
+            mt = fmaxf(mt, v);
+          }
+      } else {
+#pragma unroll
+        for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            s[jt][r] *= sl2;
+            mt = fmaxf(mt, s[jt][r]);
+          }
+      }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mn = fmaxf(m, mt);
+      // a lane whose query precedes every key of the tile keeps mn = m; its
+      // first tile (key 0) always has a visible key, so mn is finite here
+      const float corr = __builtin_amdgcn_exp2f(m - mn);
+      float ls = 0.f;
+#pragma unroll
+      for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float p = __builtin_amdgcn_exp2f(s[jt][r] - mn);
+          s[jt][r] = p;
+          ls += p;
+        }
+      ls += __shfl_xor(ls, 32, 64);
+      l = l * corr + ls;
+      m = mn;
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) ot[dt][r] *= corr;
+#pragma unroll
+      for (int jt = 0; jt < 2; jt++)
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+          const int r0 = 8 * kk;
+          const bf16x8_t pb = bf16x8_t{(__bf16)s[jt][r0 + 0], (__bf16)s[jt][r0 + 1], (__bf16)s[jt][r0 + 2],
+                                       (__bf16)s[jt][r0 + 3], (__bf16)s[jt][r0 + 4], (__bf16)s[jt][r0 + 5],
+                                       (__bf16)s[jt][r0 + 6], (__bf16)s[jt][r0 + 7]};
+#pragma unroll
+          for (int dt = 0; dt < 2; dt++) {
+            const bf16x8_t a =
+                *reinterpret_cast<const bf16x8_t*>(&Vt[buf][dt * 32 + (lane & 31)][jt * 32 + kk * 16 + 8 * half]);
+            ot[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb, ot[dt], 0, 0, 0);
+          }
+        }
+    }
+    if (kt + 1 < nkt) put(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (q >= T) return;
+  const float inv = 1.f / l;
+  bf16_t* orow = o + (size_t)(b * T + q) * d + h * HD;
+#pragma unroll
+  for (int dt = 0; dt < 2; dt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      // elements 4g .. 4g+3 are dims dt*32 + 8g + 4*half + 0..3
+      typedef __bf16 bf16x4_t_ __attribute__((ext_vector_type(4)));
+      const bf16x4_t_ v = bf16x4_t_{(__bf16)(ot[dt][4 * g] * inv), (__bf16)(ot[dt][4 * g + 1] * inv),
+                                    (__bf16)(ot[dt][4 * g + 2] * inv), (__bf16)(ot[dt][4 * g + 3] * inv)};
+      *reinterpret_cast<bf16x4_t_*>(orow + dt * 32 + 8 * g + 4 * half) = v;
+    }
+}
+
 }  // namespace
 
 template <typename KT, typename OT>
@@ -251,8 +428,9 @@ hipError_t launch_attn_prefill_mfma_q16(hipStream_t st, const bf16_t* q, int B, 
                                         const bf16_t* kcache, const bf16_t* vcache, bf16_t* o) {
   if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !q || !kcache || !vcache || !o)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((k_attn_prefill_mfma<bf16_t, bf16_t, bf16_t>), dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st,
-                     q, d, T, d, H, ctx, kcache, vcache, o);
+  if ((size_t)T * HD * 2 > 0x7fffffffu) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_prefill_bf16, dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, q, T, d, H, ctx, kcache,
+                     vcache, o);
   return hipGetLastError();
 }
 
