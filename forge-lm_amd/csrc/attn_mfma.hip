@@ -54,6 +54,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
   const float scale = 0.125f;              // 1 / sqrt(64), exact
   const KT* K = kc + ((size_t)b * H + h) * ctx * HD;
   const KT* V = vc + ((size_t)b * H + h) * ctx * HD;
+  // the first T cache rows of this (sequence, head): rows at or past T read as
+  // zeros, with no branch around the loads
+  const __amdgpu_buffer_rsrc_t rk =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<KT*>(K), (short)0, T * HD * (int)sizeof(KT), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<KT*>(V), (short)0, T * HD * (int)sizeof(KT), 0x00020000);
 
   // this lane's q (row q, clamped for the loads)
   const QT* qrow = qp + (size_t)(b * T + min(q, T - 1)) * qstride + h * HD;
@@ -96,11 +102,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         const int idx = tid + 256 * i, key = idx / 8, q8 = idx % 8;  // 8 x 8 bf16 per key row
-        uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = kv;
-        if (k0 + key < T) {
-          kv = *reinterpret_cast<const uint4*>(K + (size_t)(k0 + key) * HD + 8 * q8);
-          vv = *reinterpret_cast<const uint4*>(V + (size_t)(k0 + key) * HD + 8 * q8);
-        }
+        const u32x4_t kw = __builtin_amdgcn_raw_buffer_load_b128(rk, ((k0 + key) * HD + 8 * q8) * 2, 0, 0);
+        const u32x4_t vw = __builtin_amdgcn_raw_buffer_load_b128(rv, ((k0 + key) * HD + 8 * q8) * 2, 0, 0);
+        const uint4 kv = make_uint4(kw.x, kw.y, kw.z, kw.w), vv = make_uint4(vw.x, vw.y, vw.z, vw.w);
         *reinterpret_cast<uint4*>(&Ks[key][8 * q8]) = kv;
         const bf16_t* vh = reinterpret_cast<const bf16_t*>(&vv);
 #pragma unroll
@@ -110,11 +114,12 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int idx = tid + 256 * i, key = idx / 16, q4 = idx % 16;  // 16 x 4 floats per key row
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-        if (k0 + key < T) {
-          kv = *reinterpret_cast<const float4*>(K + (size_t)(k0 + key) * HD + 4 * q4);
-          vv = *reinterpret_cast<const float4*>(V + (size_t)(k0 + key) * HD + 4 * q4);
-        }
+        const u32x4_t kw = __builtin_amdgcn_raw_buffer_load_b128(rk, ((k0 + key) * HD + 4 * q4) * 4, 0, 0);
+        const u32x4_t vw = __builtin_amdgcn_raw_buffer_load_b128(rv, ((k0 + key) * HD + 4 * q4) * 4, 0, 0);
+        const float4 kv = make_float4(__uint_as_float(kw.x), __uint_as_float(kw.y), __uint_as_float(kw.z),
+                                      __uint_as_float(kw.w));
+        const float4 vv = make_float4(__uint_as_float(vw.x), __uint_as_float(vw.y), __uint_as_float(vw.z),
+                                      __uint_as_float(vw.w));
         // dims 4q4 .. +3: even ones to 2q4, 2q4+1; odd ones to 32 + 2q4, +1
         Ks[key][2 * q4] = kv.x;
         Ks[key][2 * q4 + 1] = kv.z;
@@ -417,7 +422,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __re
 template <typename KT, typename OT>
 hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int T, int d, int H, int ctx,
                                     const KT* kcache, const KT* vcache, OT* o) {
-  if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !qkv || !kcache || !vcache || !o)
+  if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !qkv || !kcache || !vcache || !o ||
+      (size_t)T * HD * sizeof(KT) > 0x7fffffffu)
     return hipErrorInvalidValue;
   hipLaunchKernelGGL((k_attn_prefill_mfma<KT, OT, float>), dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, qkv,
                      3 * d, T, d, H, ctx, kcache, vcache, o);

@@ -30,6 +30,7 @@ constexpr int BK = 32;   // k per stage
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 template <typename WT>
 struct Tr;
@@ -48,7 +49,11 @@ struct Tr<float> {
   typedef float elem;
 };
 
-template <typename WT, int BM, int EPI, bool RES>
+// NSR == 0: K streams through a double-buffered LDS pair, one stage ahead.
+// NSR > 0 (short K chunks of split-K decode GEMMs, at most NSR stages): every
+// stage's loads are issued at once into NSR register sets and LDS buffers, so
+// the block pays one memory latency instead of one per stage.
+template <typename WT, int BM, int EPI, bool RES, int NSR>
 __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, int M, int K,
                                                   const WT* __restrict__ Wt, int N, int kchunk,
                                                   const float* __restrict__ bias,
@@ -57,8 +62,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
   using E = typename Tr<WT>::elem;
   constexpr int LDK = Tr<WT>::LDK;
   constexpr int MT = BM / 32;  // MFMA tiles along M per wave
-  __shared__ __align__(16) E As[2][BM][LDK];
-  __shared__ __align__(16) E Bs[2][BN][LDK];
+  constexpr int NBUF = NSR > 0 ? NSR : 2;
+  constexpr int NREG = NSR > 0 ? NSR : 1;
+  __shared__ __align__(16) E As[NBUF][BM][LDK];
+  __shared__ __align__(16) E Bs[NBUF][BN][LDK];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
@@ -69,35 +76,42 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
   constexpr int AV = BM * BK / 4 / 256;  // float4 of A per thread per stage
   constexpr int WB = BN * BK * (int)sizeof(WT) / 16 / 256;  // 16-byte pieces of W per thread per stage
   static_assert(AV >= 1 && WB >= 1, "tile too small for 256 threads");
-  float4 ra[AV];
-  uint4 rw[WB];
-  auto gload = [&](int k0) {
+  float4 ra[NREG][AV];
+  uint4 rw[NREG][WB];
+  // bounded buffer resources over this block's rows of A and Wt: rows past M
+  // (N) read as zeros, with no branch around the loads (a branch would make the
+  // compiler wait for each load before the next one)
+  const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(A + (size_t)m0 * K), (short)0, min(BM, M - m0) * K * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<WT*>(Wt + (size_t)n0 * K), (short)0, min(BN, N - n0) * K * (int)sizeof(WT), 0x00020000);
+  auto gload = [&](float4 (&a)[AV], uint4 (&wv)[WB], int k0) {
 #pragma unroll
     for (int i = 0; i < AV; i++) {
       const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
-      ra[i] = (m0 + row < M) ? *reinterpret_cast<const float4*>(A + (size_t)(m0 + row) * K + k0 + 4 * kq)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsa, (row * K + k0 + 4 * kq) * 4, 0, 0);
+      a[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
     }
     constexpr int PER_ROW = BK * (int)sizeof(WT) / 16;  // 16-byte pieces per W row and stage
 #pragma unroll
     for (int i = 0; i < WB; i++) {
       const int idx = tid + 256 * i, row = idx / PER_ROW, q = idx % PER_ROW;
-      rw[i] = (n0 + row < N) ? *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(Wt + (size_t)(n0 + row) * K + k0) + 16 * q)
-                             : make_uint4(0u, 0u, 0u, 0u);
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsw, (row * K + k0) * (int)sizeof(WT) + 16 * q, 0, 0);
+      wv[i] = make_uint4(v.x, v.y, v.z, v.w);
     }
   };
-  auto sstore = [&](int b) {
+  auto sstore = [&](int b, const float4 (&a)[AV], const uint4 (&wv)[WB]) {
 #pragma unroll
     for (int i = 0; i < AV; i++) {
       const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
       if constexpr (sizeof(WT) == 2) {
-        const uint32_t lo = (uint32_t)f32_to_bf16(ra[i].x) | ((uint32_t)f32_to_bf16(ra[i].y) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16(ra[i].z) | ((uint32_t)f32_to_bf16(ra[i].w) << 16);
+        const uint32_t lo = (uint32_t)f32_to_bf16(a[i].x) | ((uint32_t)f32_to_bf16(a[i].y) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16(a[i].z) | ((uint32_t)f32_to_bf16(a[i].w) << 16);
         *reinterpret_cast<uint2*>(&As[b][row][4 * kq]) = make_uint2(lo, hi);
       } else {
         // k = 4kq .. 4kq+3: even k to positions 2kq, 2kq+1; odd k to BK/2 + 2kq, +1
-        *reinterpret_cast<float2*>(&As[b][row][2 * kq]) = make_float2(ra[i].x, ra[i].z);
-        *reinterpret_cast<float2*>(&As[b][row][BK / 2 + 2 * kq]) = make_float2(ra[i].y, ra[i].w);
+        *reinterpret_cast<float2*>(&As[b][row][2 * kq]) = make_float2(a[i].x, a[i].z);
+        *reinterpret_cast<float2*>(&As[b][row][BK / 2 + 2 * kq]) = make_float2(a[i].y, a[i].w);
       }
     }
     constexpr int PER_ROW = BK * (int)sizeof(WT) / 16;
@@ -105,10 +119,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
     for (int i = 0; i < WB; i++) {
       const int idx = tid + 256 * i, row = idx / PER_ROW, q = idx % PER_ROW;
       if constexpr (sizeof(WT) == 2) {
-        *reinterpret_cast<uint4*>(&Bs[b][row][8 * q]) = rw[i];
+        *reinterpret_cast<uint4*>(&Bs[b][row][8 * q]) = wv[i];
       } else {
-        const float4 v = make_float4(__uint_as_float(rw[i].x), __uint_as_float(rw[i].y), __uint_as_float(rw[i].z),
-                                     __uint_as_float(rw[i].w));
+        const float4 v = make_float4(__uint_as_float(wv[i].x), __uint_as_float(wv[i].y), __uint_as_float(wv[i].z),
+                                     __uint_as_float(wv[i].w));
         *reinterpret_cast<float2*>(&Bs[b][row][2 * q]) = make_float2(v.x, v.z);
         *reinterpret_cast<float2*>(&Bs[b][row][BK / 2 + 2 * q]) = make_float2(v.y, v.w);
       }
@@ -122,14 +136,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
     for (int r = 0; r < 16; r++) acc[t][r] = 0.f;
 
   const int fr = lane & 31, fh = lane >> 5;  // fragment row / column and k half
-  if (nst > 0) {
-    gload(kb);
-    sstore(0);
-  }
-  __syncthreads();
-  for (int st = 0; st < nst; st++) {
-    const int b = st & 1;
-    if (st + 1 < nst) gload(kb + (st + 1) * BK);
+  auto compute = [&](int b) {
     if constexpr (sizeof(WT) == 2) {
 #pragma unroll
       for (int kk = 0; kk < BK / 16; kk++) {
@@ -158,8 +165,31 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
         }
       }
     }
-    if (st + 1 < nst) sstore(b ^ 1);
+  };
+
+  if constexpr (NSR > 0) {
+    // stages past the chunk re-read its last stage (never multiplied): no branches around the loads
+#pragma unroll
+    for (int s2 = 0; s2 < NSR; s2++) gload(ra[s2], rw[s2], kb + min(s2, nst - 1) * BK);
+#pragma unroll
+    for (int s2 = 0; s2 < NSR; s2++) sstore(s2, ra[s2], rw[s2]);
     __syncthreads();
+#pragma unroll
+    for (int s2 = 0; s2 < NSR; s2++)
+      if (s2 < nst) compute(s2);
+  } else {
+    if (nst > 0) {
+      gload(ra[0], rw[0], kb);
+      sstore(0, ra[0], rw[0]);
+    }
+    __syncthreads();
+    for (int st = 0; st < nst; st++) {
+      const int b = st & 1;
+      if (st + 1 < nst) gload(ra[0], rw[0], kb + (st + 1) * BK);
+      compute(b);
+      if (st + 1 < nst) sstore(b ^ 1, ra[0], rw[0]);
+      __syncthreads();
+    }
   }
 
   const int col = n0 + w * 32 + fr;
@@ -202,22 +232,22 @@ hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt) {
 }
 
 // the epilogue (GELU or not, residual or not) is a template parameter of the kernel
-template <typename WT, int BM>
+template <typename WT, int BM, int NSR>
 static hipError_t launch_epi(hipStream_t st, dim3 grid, const float* a, int M, int K, const WT* Wt, int N, int kchunk,
                              const float* bias, int epi, const float* res, float* y, float* part) {
   const bool gelu = epi == EPI_GELU;
   if (part || (!gelu && !res))
-    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, false>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
-                       res, y, part);
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, false, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
+                       bias, res, y, part);
   else if (!gelu)
-    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, true>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
-                       res, y, part);
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, true, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
+                       bias, res, y, part);
   else if (!res)
-    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, false>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
-                       res, y, part);
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, false, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
+                       bias, res, y, part);
   else
-    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, true>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk, bias,
-                       res, y, part);
+    hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, true, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
+                       bias, res, y, part);
   return hipGetLastError();
 }
 
@@ -225,6 +255,8 @@ template <typename WT>
 hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, const float* bias,
                             int epi, const float* res, float* y, float* part, size_t part_floats, int cus) {
   if (!a || !Wt || !y || M <= 0 || N <= 0 || K <= 0 || K % BK != 0) return hipErrorInvalidValue;
+  // byte offsets inside a block's rows of A and Wt are 32-bit
+  if ((size_t)128 * K * 4 > 0x7fffffffu) return hipErrorInvalidValue;
   const int gn = (N + BN - 1) / BN;
   const int bm = M > 64 ? 128 : (M > 32 ? 64 : 32);
   const int gm = (M + bm - 1) / bm;
@@ -236,13 +268,17 @@ hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const 
   const int kchunk = K / S;
   dim3 grid(gn, gm, S);
   float* pp = S > 1 ? part : nullptr;
+  // chunks of at most 3 stages (split-K decode GEMMs) load all their stages at once
+  const bool resident = kchunk <= 3 * BK;
   hipError_t e;
   if (bm == 128)
-    e = launch_epi<WT, 128>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+    e = launch_epi<WT, 128, 0>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   else if (bm == 64)
-    e = launch_epi<WT, 64>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+    e = resident ? launch_epi<WT, 64, 3>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp)
+                 : launch_epi<WT, 64, 0>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   else
-    e = launch_epi<WT, 32>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
+    e = resident ? launch_epi<WT, 32, 3>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp)
+                 : launch_epi<WT, 32, 0>(st, grid, a, M, K, Wt, N, kchunk, bias, epi, res, y, pp);
   if (e != hipSuccess || S == 1) return e;
   return launch_splitk_epilogue(st, part, S, M, N, bias, epi, res, y);
 }

@@ -180,7 +180,8 @@ __global__ __launch_bounds__(256) void k_gemv_splitk(const float* __restrict__ x
       load_vec<WT, VEC>(W + (size_t)k * N + c0, wvv);
 #pragma unroll
       for (int m = 0; m < MR; m++) {
-        const float xm = (m < M) ? x[(size_t)m * K + k] : 0.f;
+        // rows past M (never stored) read row M - 1: no branch around the load
+        const float xm = x[(size_t)min(m, M - 1) * K + k];
 #pragma unroll
         for (int j = 0; j < VEC; j++) acc[m][j] += xm * wvv[j];
       }
@@ -206,6 +207,8 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
   if (idx >= (size_t)M * N) return;
   const int n = (int)(idx % N);
   float s = 0.f;
+  // partials summed in order; the unrolled loads of a batch are independent and go out together
+#pragma unroll 8
   for (int i = 0; i < S; i++) s += part[(size_t)i * M * N + idx];
   if (bias) s += bias[n];
   if (epi == EPI_GELU) s = gelu_tanh(s);
@@ -445,6 +448,7 @@ namespace {
 constexpr int kST = 1024;        // sampler block size
 constexpr int kMaxVocab = 65536; // LDS bitmaps hold V bits
 constexpr int kSurvCap = 4096;   // top-k survivors summed in index order
+constexpr int kRowV = 16;        // logits per thread in the register sampler (V <= kST * kRowV)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -563,6 +567,491 @@ __device__ int block_exclusive_scan(int v, int& excl, SampleSmem& sm) {
 }
 
 }  // namespace
+
+// ---- register sampler for V <= kST * kRowV (the configurations' 16384) -------------
+// The same steps and arithmetic as k_sample, with thread t holding logits
+// 16t .. 16t+15 in registers (index order = thread order, then register order):
+// bans and penalties are applied from LDS bitmaps, reductions are wave DPP /
+// shuffle steps plus one LDS exchange of the 16 wave results, the top-k threshold
+// is a two-bits-per-pass radix select over register keys, and the top-k survivors'
+// sequential sum and CDF walk run on one wave (expf in parallel, the fold in index
+// order through readlane).  The all-vocabulary path keeps k_sample's per-thread
+// partial sums folded in thread order.
+
+// x lies in the candidate window [lo, max] (lo finite; -inf and NaN never do)
+__device__ __forceinline__ bool dlt_ok(float x, float lo) { return x >= lo; }
+
+// integer wave sum through DPP row shifts and a row broadcast, result in every lane
+__device__ __forceinline__ int wave_sum_int_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row half mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row broadcast 15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row broadcast 31
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+struct SampleRowSmem {
+  uint32_t seen[kST * kRowV / 32];
+  uint32_t ban[kST * kRowV / 32];
+  float redf[2][kST / 64];
+  int redi[2][kST / 64];
+  int cntp[2][kST / 64][2];
+  int wscan[kST / 64];
+  uint32_t ckey[1024];
+  int ladder[8][kST / 64];
+  int surv[kSurvCap];
+  float survv[kSurvCap];
+  float part[kST];
+  int misc[4];
+};
+
+// block max of one value per thread (all threads get it); slot alternates between calls
+__device__ __forceinline__ float row_block_max(float v, SampleRowSmem& sm, int slot) {
+  v = wave_max(v);
+  if ((threadIdx.x & 63) == 0) sm.redf[slot][threadIdx.x >> 6] = v;
+  __syncthreads();
+  float r = sm.redf[slot][0];
+#pragma unroll
+  for (int i = 1; i < kST / 64; i++) r = fmaxf(r, sm.redf[slot][i]);
+  return r;
+}
+
+__device__ __forceinline__ int row_block_argmax(const float (&x)[kRowV], int V, SampleRowSmem& sm, int slot) {
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int j = 0; j < kRowV; j++) {
+    const int i = threadIdx.x * kRowV + j;
+    if (i < V) argmax_merge(best, bi, x[j], i);
+  }
+  wave_argmax(best, bi);
+  if ((threadIdx.x & 63) == 0) {
+    sm.redf[slot][threadIdx.x >> 6] = best;
+    sm.redi[slot][threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  float bv = sm.redf[slot][0];
+  int ii = sm.redi[slot][0];
+#pragma unroll
+  for (int i = 1; i < kST / 64; i++) argmax_merge(bv, ii, sm.redf[slot][i], sm.redi[slot][i]);
+  if (ii == 0x7fffffff) ii = 0;  // all NaN: Greedy keeps index 0
+  return ii;
+}
+
+__global__ __launch_bounds__(kST) void k_sample_row(SampleArgs a) {
+  __shared__ SampleRowSmem sm;
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, V = a.V;
+  const int n = *a.step;
+  const float* lg = a.logits + (size_t)b * V;
+  const int total = a.prompt_len + n;
+  const int T = min(total, a.ctx);
+  const int* hist = a.tokens + (size_t)b * a.tok_stride + (total - T);
+  if (a.dump && n < a.max_new)
+    for (int i = tid; i < V; i += kST) a.dump[((size_t)b * a.max_new + n) * V + i] = lg[i];
+  float x[kRowV];
+  if ((V & 3) == 0 && (reinterpret_cast<uintptr_t>(lg) & 15) == 0) {
+    // 16-byte loads; groups past V load the last group and drop it (no branch around the loads)
+#pragma unroll
+    for (int q = 0; q < kRowV / 4; q++) {
+      const int i = tid * kRowV + 4 * q;
+      const float4 v = *reinterpret_cast<const float4*>(lg + min(i, V - 4));
+      x[4 * q] = v.x;
+      x[4 * q + 1] = v.y;
+      x[4 * q + 2] = v.z;
+      x[4 * q + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kRowV; j++) x[j] = lg[min(tid * kRowV + j, V - 1)];
+  }
+#pragma unroll
+  for (int j = 0; j < kRowV; j++)
+    if (tid * kRowV + j >= V) x[j] = -INFINITY;
+  const bool controls = (a.penalty != 1.f) || (a.ngram > 0);
+  const bool sampling = a.temperature > 0.f;
+  int result = 0;
+  if (!controls && !sampling) {
+    result = row_block_argmax(x, V, sm, 0);
+  } else {
+    if (a.penalty != 1.f) {  // Sampler.cs:117-127: each distinct id of the window once
+      for (int i = tid; i < kST * kRowV / 32; i += kST) sm.seen[i] = 0;
+      __syncthreads();
+      for (int i = tid; i < T; i += kST) {
+        const int t = hist[i];
+        if ((unsigned)t < (unsigned)V) atomicOr(&sm.seen[t >> 5], 1u << (t & 31));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kRowV; j++) {
+        const int i = tid * kRowV + j;
+        if ((sm.seen[i >> 5] >> (i & 31)) & 1u) x[j] = x[j] < 0.f ? x[j] * a.penalty : x[j] / a.penalty;
+      }
+    }
+    if (a.ngram > 0 && T >= a.ngram - 1) {  // Sampler.cs:129-164
+      for (int i = tid; i < kST * kRowV / 32; i += kST) sm.ban[i] = 0;
+      __syncthreads();
+      const int ng = a.ngram;
+      if (ng == 1) {
+        for (int i = tid; i < T; i += kST) {
+          const int t = hist[i];
+          if ((unsigned)t < (unsigned)V) atomicOr(&sm.ban[t >> 5], 1u << (t & 31));
+        }
+      } else {
+        const int pre = ng - 1, suf = T - pre;
+        for (int s0 = tid; s0 + ng <= T; s0 += kST) {
+          bool match = true;
+          for (int j = 0; j < pre; j++)
+            if (hist[s0 + j] != hist[suf + j]) {
+              match = false;
+              break;
+            }
+          const int t = hist[s0 + pre];
+          if (match && (unsigned)t < (unsigned)V) atomicOr(&sm.ban[t >> 5], 1u << (t & 31));
+        }
+      }
+      __syncthreads();
+      // all banned (or -inf): Sampler.cs:156-164 keeps the post-penalty logits
+      int avail = 0;
+#pragma unroll
+      for (int j = 0; j < kRowV; j++) {
+        const int i = tid * kRowV + j;
+        if (i < V && !((sm.ban[i >> 5] >> (i & 31)) & 1u) && !(x[j] == -INFINITY)) avail = 1;
+      }
+      avail = __syncthreads_or(avail);
+      if (avail) {
+#pragma unroll
+        for (int j = 0; j < kRowV; j++) {
+          const int i = tid * kRowV + j;
+          if ((sm.ban[i >> 5] >> (i & 31)) & 1u) x[j] = -INFINITY;
+        }
+      }
+    }
+    if (!sampling) {
+      result = row_block_argmax(x, V, sm, 1);
+    } else {
+#pragma unroll
+      for (int j = 0; j < kRowV; j++) x[j] = x[j] / a.temperature;
+      const bool filt = a.top_k > 0 && a.top_k < V;
+      float thr = -INFINITY;
+      if (filt) {
+        // k-th largest (duplicates counted) by a radix select on order keys,
+        // two bits a pass; absent entries hold key 0, below every real key
+        uint32_t key[kRowV];
+#pragma unroll
+        for (int j = 0; j < kRowV; j++) key[j] = (tid * kRowV + j < V) ? order_key(x[j]) : 0u;
+        uint32_t prefix = 0;
+        int rem = a.top_k;
+        int nin = kST * kRowV;  // slots whose key matches the prefix (absent slots included)
+        // the k-th largest key's digit among counts c1..c3 (digit 0 takes the rest)
+        auto choose = [&](int t1, int t2, int t3) -> uint32_t {
+          if (t3 >= rem) return nin = t3, 3u;
+          rem -= t3;
+          if (t2 >= rem) return nin = t2, 2u;
+          rem -= t2;
+          if (t1 >= rem) return nin = t1, 1u;
+          rem -= t1;
+          nin = nin - t1 - t2 - t3;
+          return 0u;
+        };
+        int sh = 30;
+        // Candidate window: with M the largest value, the first t of a ladder
+        // for which [M - t, M] holds at least k values contains the k-th largest;
+        // when it holds at most 1024 they are gathered for the wave-0 passes and
+        // the block-wide passes are skipped (the selection stays exact).
+        float lo = -INFINITY;
+        {
+          float lm = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < kRowV; j++) lm = fmaxf(lm, x[j]);
+          const float M = row_block_max(lm, sm, 1);
+          if (M > -INFINITY && M < INFINITY) {
+            int cl[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) cl[q] = 0;
+            // window q is x >= M - 2^q / 8; the same lower bound gathers it below
+            // (NaN and absent -inf entries are in no window)
+#pragma unroll
+            for (int j = 0; j < kRowV; j++) {
+#pragma unroll
+              for (int q = 0; q < 8; q++) cl[q] += dlt_ok(x[j], M - (float)(1 << q) * 0.125f) ? 1 : 0;
+            }
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+              cl[q] = wave_sum_int_dpp(cl[q]);
+              if (lane == 0) sm.ladder[q][wv] = cl[q];
+            }
+            __syncthreads();
+            int pick = -1;
+            for (int q = 0; q < 8 && pick < 0; q++) {
+              int tot = 0;
+              for (int w2 = 0; w2 < kST / 64; w2++) tot += sm.ladder[q][w2];
+              if (tot >= a.top_k) pick = tot <= 1024 ? q : 8;
+            }
+            if (pick >= 0 && pick < 8) lo = M - (float)(1 << pick) * 0.125f;
+          }
+        }
+        if (lo > -INFINITY) {
+          // gather the window's keys; the prefix starts empty and the wave passes do every bit
+          int cnt = 0;
+#pragma unroll
+          for (int j = 0; j < kRowV; j++) cnt += (dlt_ok(x[j], lo)) ? 1 : 0;
+          int incl = cnt;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+          }
+          if (lane == 63) sm.wscan[wv] = incl;
+          __syncthreads();
+          int off = incl - cnt;
+          nin = 0;
+          for (int w2 = 0; w2 < kST / 64; w2++) {
+            if (w2 < wv) off += sm.wscan[w2];
+            nin += sm.wscan[w2];
+          }
+#pragma unroll
+          for (int j = 0; j < kRowV; j++)
+            if (dlt_ok(x[j], lo)) sm.ckey[off++] = key[j];
+          __syncthreads();
+        }
+        // block-wide passes while many keys still match the prefix
+        for (; lo == -INFINITY && sh >= 0 && nin > 1024; sh -= 2) {
+          const uint32_t hm = sh == 30 ? 0u : (0xffffffffu << (sh + 2));
+          // counts of digits 1 and 2 packed in 16-bit fields, digit 3 apart (a wave
+          // counts at most 1024 and the block at most 16384 of each)
+          int c12 = 0, c3 = 0;
+#pragma unroll
+          for (int j = 0; j < kRowV; j++) {
+            const uint32_t d = (key[j] >> sh) & 3u;
+            const bool in = (key[j] & hm) == prefix;
+            c12 += (in && d == 1u) ? 1 : ((in && d == 2u) ? 0x10000 : 0);
+            c3 += (in && d == 3u) ? 1 : 0;
+          }
+          c12 = wave_sum_int_dpp(c12);
+          c3 = wave_sum_int_dpp(c3);
+          const int slot = (sh >> 1) & 1;  // rewritten two passes later, after the next barrier
+          if (lane == 0) {
+            sm.cntp[slot][wv][0] = c12;
+            sm.cntp[slot][wv][1] = c3;
+          }
+          __syncthreads();
+          int t12 = 0, t3 = 0;
+#pragma unroll
+          for (int w2 = 0; w2 < kST / 64; w2++) {
+            t12 += sm.cntp[slot][w2][0];
+            t3 += sm.cntp[slot][w2][1];
+          }
+          const int t1 = t12 & 0xffff, t2 = (int)((uint32_t)t12 >> 16);
+          prefix |= choose(t1, t2, t3) << sh;
+        }
+        if (sh >= 0 && lo == -INFINITY) {
+          // at most 1024 keys match: gather them into LDS (any order) and finish
+          // the remaining passes on wave 0 alone, without block barriers
+          const uint32_t hm = sh == 30 ? 0u : (0xffffffffu << (sh + 2));
+          int cnt = 0;
+#pragma unroll
+          for (int j = 0; j < kRowV; j++) cnt += (key[j] & hm) == prefix ? 1 : 0;
+          int incl = cnt;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+          }
+          if (lane == 63) sm.wscan[wv] = incl;
+          __syncthreads();
+          int off = incl - cnt;
+          for (int w2 = 0; w2 < wv; w2++) off += sm.wscan[w2];
+#pragma unroll
+          for (int j = 0; j < kRowV; j++)
+            if ((key[j] & hm) == prefix) sm.ckey[off++] = key[j];
+          __syncthreads();
+        }
+        if (sh >= 0) {
+          if (wv == 0) {
+            constexpr int E = 1024 / 64;
+            const int ne = (nin + 63) >> 6;  // filled key groups (uniform)
+            uint32_t ck[E];
+            bool ok[E];
+            uint32_t kand = 0xffffffffu, kor = 0u;
+#pragma unroll
+            for (int e = 0; e < E; e++) {
+              ok[e] = lane + 64 * e < nin;
+              ck[e] = sm.ckey[min(lane + 64 * e, 1023)];
+              if (ok[e]) {
+                kand &= ck[e];
+                kor |= ck[e];
+              }
+            }
+            // bits every gathered key shares (below the prefix already fixed) are
+            // the k-th largest's too: take them and start at the first digit that differs
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+              kand &= (uint32_t)__shfl_xor((int)kand, o, 64);
+              kor |= (uint32_t)__shfl_xor((int)kor, o, 64);
+            }
+            const uint32_t diff = kand ^ kor;
+            const uint32_t low = sh >= 30 ? 0xffffffffu : ((1u << (sh + 2)) - 1u);  // bits not yet fixed
+            if (nin > 0) {
+              const int top = diff & low ? 31 - __builtin_clz(diff & low) : -1;  // highest differing bit
+              const int shd = top < 0 ? -2 : (top & ~1);                         // its 2-bit digit
+              const uint32_t fixed = top < 0 ? low : (low & ~((1u << (shd + 2)) - 1u));
+              prefix |= kand & fixed;
+              sh = min(sh, shd);
+            }
+            for (; sh >= 0; sh -= 2) {
+              const uint32_t hm2 = sh == 30 ? 0u : (0xffffffffu << (sh + 2));  // no 32-bit shift
+              int c12 = 0, c3 = 0;
+#pragma unroll
+              for (int e = 0; e < E; e++) {
+                if (e >= ne) break;
+                const uint32_t d = (ck[e] >> sh) & 3u;
+                const bool in = ok[e] && (ck[e] & hm2) == prefix;
+                c12 += (in && d == 1u) ? 1 : ((in && d == 2u) ? 0x10000 : 0);
+                c3 += (in && d == 3u) ? 1 : 0;
+              }
+              c12 = wave_sum_int_dpp(c12);
+              c3 = wave_sum_int_dpp(c3);
+              prefix |= choose(c12 & 0xffff, (int)((uint32_t)c12 >> 16), c3) << sh;
+            }
+            if (lane == 0) sm.misc[1] = (int)prefix;
+          }
+          __syncthreads();
+          prefix = (uint32_t)sm.misc[1];
+        }
+        thr = key_to_float(prefix);
+      }
+      float p[kRowV];
+      float lmx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kRowV; j++) {
+        p[j] = (tid * kRowV + j >= V || (filt && x[j] < thr)) ? -INFINITY : x[j];
+        lmx = fmaxf(lmx, p[j]);
+      }
+      const float mx = row_block_max(lmx, sm, 0);
+      const double u01 = a.uniforms ? a.uniforms[(size_t)b * a.max_new + n] : 0.0;
+      int nsurv = 0;
+      if (filt) {
+        // survivors (x >= thr) in index order: per-thread counts, wave scan, wave offsets
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kRowV; j++) cnt += (tid * kRowV + j < V && x[j] >= thr) ? 1 : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int t = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += t;
+        }
+        if (lane == 63) sm.wscan[wv] = incl;
+        __syncthreads();
+        int before = 0;
+        for (int w2 = 0; w2 < kST / 64; w2++) {
+          const int c = sm.wscan[w2];
+          if (w2 < wv) before += c;
+          nsurv += c;
+        }
+        if (nsurv <= kSurvCap) {
+          int off = before + incl - cnt;
+#pragma unroll
+          for (int j = 0; j < kRowV; j++)
+            if (tid * kRowV + j < V && x[j] >= thr) {
+              sm.surv[off] = tid * kRowV + j;
+              sm.survv[off] = x[j];
+              off++;
+            }
+        }
+        __syncthreads();
+      }
+      if (filt && nsurv <= kSurvCap) {
+        // exact reference order: the sum and the CDF walk over the survivors in
+        // index order; wave 0 computes the exps in parallel and folds them in order
+        if (wv == 0) {
+          float sum = 0.f;
+          for (int c0 = 0; c0 < nsurv; c0 += 64) {
+            const float e = (c0 + lane < nsurv) ? expf(sm.survv[c0 + lane] - mx) : 0.f;
+            const int m = min(64, nsurv - c0);
+            for (int q = 0; q < m; q++) sum = sum + __shfl(e, q, 64);
+          }
+          const float u = (float)u01 * sum;
+          float acc = 0.f;
+          int r = V - 1;
+          bool found = false;
+          for (int c0 = 0; c0 < nsurv && !found; c0 += 64) {
+            const float e = (c0 + lane < nsurv) ? expf(sm.survv[c0 + lane] - mx) : 0.f;
+            const int m = min(64, nsurv - c0);
+            for (int q = 0; q < m; q++) {
+              acc = acc + __shfl(e, q, 64);
+              if (u < acc) {
+                r = sm.surv[c0 + q];
+                found = true;
+                break;
+              }
+            }
+          }
+          if (lane == 0) sm.misc[3] = r;
+        }
+        __syncthreads();
+        result = sm.misc[3];
+      } else {
+        // all-vocabulary CDF: per-thread sequential partial sums combined in
+        // thread order (rounding may differ from one sequential pass)
+        float ls = 0.f;
+#pragma unroll
+        for (int j = 0; j < kRowV; j++)
+          if (tid * kRowV + j < V) ls = ls + expf(p[j] - mx);
+        sm.part[tid] = ls;
+        __syncthreads();
+        if (wv == 0) {
+          // the same thread-order fold, one partial per readlane, keeping each
+          // thread's exclusive prefix
+          float run = 0.f;
+          for (int c0 = 0; c0 < kST; c0 += 64) {
+            const int v = __float_as_int(sm.part[c0 + lane]);
+            float pre = 0.f;
+#pragma unroll
+            for (int q = 0; q < 64; q++) {
+              pre = lane == q ? run : pre;
+              run = run + __int_as_float(__builtin_amdgcn_readlane(v, q));
+            }
+            sm.part[c0 + lane] = pre;
+          }
+          if (lane == 0) {
+            sm.misc[0] = __float_as_int(run);
+            sm.misc[3] = 0x7fffffff;
+          }
+        }
+        __syncthreads();
+        const float u = (float)u01 * __int_as_float(sm.misc[0]);
+        float acc = sm.part[tid];
+        int cand = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kRowV; j++) {
+          if (tid * kRowV + j < V && cand == 0x7fffffff) {
+            acc = acc + expf(p[j] - mx);
+            if (u < acc) cand = tid * kRowV + j;
+          }
+        }
+        if (cand != 0x7fffffff) atomicMin(&sm.misc[3], cand);
+        __syncthreads();
+        result = sm.misc[3] == 0x7fffffff ? V - 1 : sm.misc[3];
+      }
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (a.prompt_len + n < a.tok_stride) a.tokens[(size_t)b * a.tok_stride + a.prompt_len + n] = result;
+    if (n < a.max_new) a.out_ids[(size_t)b * a.max_new + n] = result;
+    if (a.out_counts[b] < 0 && a.eos >= 0 && result == a.eos) a.out_counts[b] = n + 1;
+    __threadfence();
+    const int prev = atomicAdd(a.done, 1);
+    if (prev == a.B - 1) {  // last block: every block has read the step already
+      *a.done = 0;
+      *a.step = n + 1;
+      __threadfence();
+    }
+  }
+}
 
 __global__ __launch_bounds__(kST) void k_sample(SampleArgs a) {
   __shared__ SampleSmem sm;
@@ -904,7 +1393,10 @@ hipError_t launch_sample(hipStream_t st, const SampleArgs& a) {
   FH_CHECK_ARG(a.B > 0 && a.V > 0 && a.V <= kMaxVocab && a.logits && a.work && a.tokens && a.step && a.done &&
                a.out_ids && a.out_counts && a.max_new > 0);
   FH_CHECK_ARG(!(a.temperature > 0.f) || a.uniforms);
-  hipLaunchKernelGGL(k_sample, dim3(a.B), dim3(kST), 0, st, a);
+  if (a.V <= kST * kRowV)
+    hipLaunchKernelGGL(k_sample_row, dim3(a.B), dim3(kST), 0, st, a);
+  else
+    hipLaunchKernelGGL(k_sample, dim3(a.B), dim3(kST), 0, st, a);
   return hipGetLastError();
 }
 

@@ -158,6 +158,28 @@ def test_sampler_exact_on_same_logits(fhp, oracle, backend):
     assert cases == 60
 
 
+@pytest.mark.parametrize("shape", ["narrow", "wide", "ties"])
+@pytest.mark.parametrize("k", [1, 30, 700, 5000])
+def test_sampler_top_k_selection(fhp, oracle, backend, shape, k):
+    """Top-k thresholds where every logit shares its top key bits (all in [2, 4)),
+    where the largest values are far apart (no narrow window around the maximum
+    holds k of them) and with heavy ties, at V = 16384: the device id equals the
+    oracle's for several uniforms."""
+    rng = np.random.default_rng(k + len(shape))
+    V = 16384
+    if shape == "narrow":
+        lg = (2.0 + 2.0 * rng.random(V)).astype(np.float32)
+    elif shape == "wide":
+        lg = (rng.standard_normal(V) * 40).astype(np.float32)
+    else:
+        lg = np.round(rng.standard_normal(V) * 3, 0).astype(np.float32)
+    dev = fhp.DeviceBuffer.from_array(backend, lg)
+    for u in (0.0, 0.37, 0.999):
+        got = fhp.Sampler.sample_device_logits(backend, dev.ptr, V, [], 0.9, k, u)
+        assert got == oracle.sample(lg, 0.9, k, u), (shape, k, u)
+    dev.free()
+
+
 def test_c3_sampling_path(fhp, oracle, backend):
     """T 0.7, top-k 30, repetition 1.1, no-repeat-ngram 4, prompt 32 + 512.
 
