@@ -34,6 +34,16 @@ namespace fh {
 void init_registry_random(int seed, int n_layers, const std::vector<int64_t>& offsets,
                           const std::vector<int64_t>& sizes, const std::vector<int>& kinds, float* w);
 void random_doubles(int seed, int n, double* out);
+struct CkptHeader {
+  int vocab = 0, ctx = 0, d = 0, layers = 0, heads = 0;
+  std::string name, arch;
+  std::vector<std::string> names;
+  bool has_training = false, has_moments = false;
+};
+std::string read_checkpoint(const char* path, CkptHeader* hdr,
+                            std::string (*registry)(const CkptHeader&, std::vector<std::string>*, int64_t*),
+                            std::vector<float>* weights, bool header_only, bool* data_error);
+void sha256(const void* data, size_t n, uint8_t out[32]);
 }
 
 using namespace fh;
@@ -895,6 +905,80 @@ int fh_session_init_random(fh_session* s, int32_t seed) {
   for (auto o : offs) ptrs.push_back(w.data() + o);
   HIP_TRY(hipSetDevice(s->ctx->device));
   return upload_weights(s, ptrs.data());
+}
+
+// ---------------------------------------------------------------------------
+// FORGEMODEL1 checkpoints (Checkpoint.Load, src/LLM.Core/Checkpoint/Checkpoint.cs:116-250)
+// ---------------------------------------------------------------------------
+extern "C++" {
+namespace {
+
+// the registry a checkpoint's header describes (ModelConfig's checks first)
+std::string ckpt_registry(const CkptHeader& h, std::vector<std::string>* names, int64_t* nparams) {
+  fh_model_desc d{h.vocab, h.ctx, h.d, h.layers, h.heads, 1, FH_DTYPE_F32, 0};
+  if (d.vocab_size <= 0) return "VocabSize must be positive.";
+  if (d.context_length <= 0) return "ContextLength must be positive.";
+  if (d.d_model <= 0) return "DModel must be positive.";
+  if (d.n_layers <= 0) return "NLayers must be positive.";
+  if (d.n_heads <= 0) return "NHeads must be positive.";
+  if (d.d_model % d.n_heads != 0)
+    return "DModel (" + std::to_string(d.d_model) + ") must be divisible by NHeads (" + std::to_string(d.n_heads) +
+           ").";
+  *nparams = 0;
+  for (auto& sl : make_registry(d)) {
+    names->push_back(sl.name);
+    *nparams += sl.numel;
+  }
+  return "";
+}
+
+}  // namespace
+}  // extern "C++"
+
+int fh_checkpoint_info(const char* path, fh_model_desc* desc, char* name, size_t name_len, int verify) {
+  if (!path || !desc) return set_err(FH_ERR_INVALID, "null argument");
+  CkptHeader h;
+  bool data_error = true;
+  const std::string e = read_checkpoint(path, &h, ckpt_registry, nullptr, verify == 0, &data_error);
+  if (!e.empty()) return set_err(data_error ? FH_ERR_DATA : FH_ERR_INVALID, "%s", e.c_str());
+  desc->vocab_size = h.vocab;
+  desc->context_length = h.ctx;
+  desc->d_model = h.d;
+  desc->n_layers = h.layers;
+  desc->n_heads = h.heads;
+  if (name && name_len) snprintf(name, name_len, "%s", h.name.c_str());
+  return FH_OK;
+}
+
+int fh_session_load_checkpoint(fh_session* s, const char* path) {
+  if (!s || !path) return set_err(FH_ERR_INVALID, "null argument");
+  CkptHeader h;
+  bool data_error = true;
+  std::vector<float> w;
+  const std::string e = read_checkpoint(path, &h, ckpt_registry, &w, false, &data_error);
+  if (!e.empty()) return set_err(data_error ? FH_ERR_DATA : FH_ERR_INVALID, "%s", e.c_str());
+  const fh_model_desc& d = s->d;
+  if (h.vocab != d.vocab_size || h.ctx != d.context_length || h.d != d.d_model || h.layers != d.n_layers ||
+      h.heads != d.n_heads)
+    return set_err(FH_ERR_INVALID,
+                   "checkpoint model (V %d, ctx %d, d %d, L %d, H %d) does not match the session's "
+                   "(V %d, ctx %d, d %d, L %d, H %d)",
+                   h.vocab, h.ctx, h.d, h.layers, h.heads, d.vocab_size, d.context_length, d.d_model, d.n_layers,
+                   d.n_heads);
+  std::vector<const float*> ptrs;
+  int64_t off = 0;
+  for (auto& sl : s->reg) {
+    ptrs.push_back(w.data() + off);
+    off += sl.numel;
+  }
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  return upload_weights(s, ptrs.data());
+}
+
+int fh_sha256(const void* data, size_t n, uint8_t* out32) {
+  if ((!data && n) || !out32) return set_err(FH_ERR_INVALID, "null argument");
+  sha256(data, n, out32);
+  return FH_OK;
 }
 
 int fh_session_load_weights(fh_session* s, const float* const* tensors, int n) {

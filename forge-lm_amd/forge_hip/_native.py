@@ -19,6 +19,7 @@ FH_ERR_HIP = -3
 FH_ERR_OOM = -4
 FH_ERR_STATE = -5
 FH_ERR_UNSUPPORTED = -6
+FH_ERR_DATA = -7
 
 FH_DTYPE_F32 = 0
 FH_DTYPE_BF16 = 1
@@ -31,6 +32,7 @@ EXPORTS = (
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_sample_logits",
+    "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256",
 )
 
 
@@ -56,6 +58,10 @@ class HipError(RuntimeError):
 
 class ArgumentError(HipError, ValueError):
     """FH_ERR_INVALID / FH_ERR_RANGE: the reference's ArgumentException family."""
+
+
+class InvalidDataError(HipError, ValueError):
+    """FH_ERR_DATA: the reference's InvalidDataException (malformed or corrupted checkpoint)."""
 
 
 _lib = None
@@ -96,6 +102,9 @@ def lib():
     L.fh_generate.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp, vp, vp, vp]
     L.fh_last_timing.argtypes = [vp, P(f64), P(f64), P(i32), P(i32)]
     L.fh_sample_logits.argtypes = [vp, vp, ctypes.c_int, vp, ctypes.c_int, P(Sampling), f64, P(i32)]
+    L.fh_checkpoint_info.argtypes = [ctypes.c_char_p, P(ModelDesc), ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int]
+    L.fh_session_load_checkpoint.argtypes = [vp, ctypes.c_char_p]
+    L.fh_sha256.argtypes = [vp, ctypes.c_size_t, vp]
     _lib = L
     return L
 
@@ -113,4 +122,6 @@ def check(code: int) -> int:
     msg = last_error()
     if code in (FH_ERR_INVALID, FH_ERR_RANGE):
         raise ArgumentError(code, msg)
+    if code == FH_ERR_DATA:
+        raise InvalidDataError(code, msg)
     raise HipError(code, msg)

@@ -44,6 +44,7 @@ extern "C" {
 #define FH_ERR_OOM (-4)         /* device allocation failed */
 #define FH_ERR_STATE (-5)       /* call out of order (e.g. generate before weights) */
 #define FH_ERR_UNSUPPORTED (-6) /* shape or option this build does not run */
+#define FH_ERR_DATA (-7)        /* malformed or corrupted file: InvalidDataException */
 
 /* weight / activation storage type of a session */
 #define FH_DTYPE_F32 0
@@ -127,6 +128,18 @@ int fh_session_init_random(fh_session* s, int32_t seed);
 int fh_session_load_weights(fh_session* s, const float* const* tensors, int n);
 /* Copies the device copy of registry tensor `index` back as fp32 (bf16 sessions widen). */
 int fh_session_read_param(fh_session* s, int index, float* out, int64_t numel);
+
+/* FORGEMODEL1 checkpoints (Checkpoint.Load / LoadCore, src/LLM.Core/Checkpoint/Checkpoint.cs:116-250).
+ * fh_checkpoint_info validates the header the way LoadCore does (magic, header length,
+ * architecture, model name, training header, ModelConfig, registry names, payload size)
+ * and, with verify != 0, the SHA-256 trailer too; it fills desc's five model fields and
+ * the model name.  fh_session_load_checkpoint reads and verifies the whole file and
+ * uploads the weights into a session of the same configuration (the optimizer moments
+ * are checksummed and dropped).  Data errors return FH_ERR_DATA with LoadCore's message. */
+int fh_checkpoint_info(const char* path, fh_model_desc* desc, char* name, size_t name_len, int verify);
+int fh_session_load_checkpoint(fh_session* s, const char* path);
+/* SHA-256 (FIPS 180-4) of n bytes, the checkpoint trailer's hash. */
+int fh_sha256(const void* data, size_t n, uint8_t* out32);
 
 /* GptModel.ForwardLast for `batch` windows of equal length T (ids[b*T + t]):
  * logits_out[b*V + v] is the last row's logits.  Full recompute, no state kept. */
