@@ -171,6 +171,25 @@ struct CachedGraph {
   hipGraphExec_t exec = nullptr;
 };
 
+namespace {
+struct StepPlan {
+  int P = 0, max_new = 0, tok_stride = 0;
+  const fh_sampling* opts = nullptr;
+  bool with_sample = true;
+};
+
+// a generation between fh_generate_begin and its last fh_generate_next (or inside fh_generate)
+struct GenState {
+  bool active = false;
+  int B = 0, P = 0, max_new = 0;
+  int next = 0;         // first step not yet enqueued (step 0 is the prompt's forward)
+  int n_dec = 0, n_re = 0;
+  bool persistent = false, dump = false, sampled = false;
+  fh_sampling opts{};
+  StepPlan plan;        // plan.opts points at opts
+};
+}  // namespace
+
 struct fh_session {
   fh_context* ctx = nullptr;
   fh_model_desc d{};
@@ -210,6 +229,8 @@ struct fh_session {
   bool bf16_act = true;      // FORGE_HIP_BF16_ACT=0 keeps a bf16 session's window GEMMs on fp32 operands
   bool counted = false;      // holds a reference on its context
   bool use_fast() const { return fast.enabled && fast_allowed; }
+  // generation in progress
+  GenState gen;
   // graphs
   CachedGraph g_decode, g_reprefill;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
@@ -397,11 +418,6 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
   return FH_OK;
 }
 
-struct StepPlan {
-  int P = 0, max_new = 0, tok_stride = 0;
-  const fh_sampling* opts = nullptr;
-  bool with_sample = true;
-};
 
 SampleArgs make_sample_args(fh_session* s, const StepPlan& p) {
   SampleArgs a{};
@@ -1026,6 +1042,7 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
   hipStream_t st = s->ctx->stream;
   FH_TRY(ensure(&s->tokens, &s->tokens_cap, (size_t)batch * T, &s->buf_gen));
   HIP_TRY(hipMemcpyAsync(s->tokens, ids, sizeof(int32_t) * batch * T, hipMemcpyHostToDevice, st));
+  s->gen.active = false;  // the forward reuses the token buffer and step state of a generation
   FH_TRY(reset_step_state(s));
   fh_sampling greedy{0.f, 0, 1.f, 0, -1, 0};
   StepPlan p;
@@ -1040,11 +1057,12 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
   return FH_OK;
 }
 
-int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
-                const double* uniforms, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
-  if (!s || !prompts || !opts || !out_ids || !out_counts) return set_err(FH_ERR_INVALID, "null argument");
+// Validation (Sampler.cs:82-89, 169-175), buffers, prompt upload and the step
+// graphs of a generation; nothing is enqueued yet.  The state lives in s->gen.
+static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
+                     const double* uniforms, bool dump) {
+  s->gen.active = false;
   if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
-  // Sampler.Generate validation, Sampler.cs:82-89, 169-175
   if (P <= 0) return set_err(FH_ERR_INVALID, "Need at least one prompt token.");
   if (max_new < 0) return set_err(FH_ERR_RANGE, "maxNewTokens must be >= 0");
   if (opts->eos_id >= s->d.vocab_size)
@@ -1057,8 +1075,16 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   if (opts->temperature > 0.f && !uniforms)
     return set_err(FH_ERR_INVALID, "sampling with temperature > 0 needs one uniform per step");
   FH_TRY(validate_ids(s, prompts, (size_t)batch * P));
-  for (int b = 0; b < batch; b++) out_counts[b] = 0;
-  if (max_new == 0) return FH_OK;
+  GenState& g = s->gen;
+  g = GenState{};
+  g.B = batch;
+  g.P = P;
+  g.max_new = max_new;
+  g.opts = *opts;
+  if (max_new == 0) {
+    g.active = true;
+    return FH_OK;
+  }
   HIP_TRY(hipSetDevice(s->ctx->device));
   hipStream_t st = s->ctx->stream;
   const int B = batch, V = s->d.vocab_size, C = s->d.context_length;
@@ -1066,23 +1092,23 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   FH_TRY(ensure(&s->tokens, &s->tokens_cap, (size_t)B * stride, &s->buf_gen));
   FH_TRY(ensure(&s->out_ids, &s->out_cap, (size_t)B * max_new, &s->buf_gen));
   if (uniforms) FH_TRY(ensure(&s->uniforms, &s->uni_cap, (size_t)B * max_new, &s->buf_gen));
-  if (logits_dump) FH_TRY(ensure(&s->dump, &s->dump_cap, (size_t)B * max_new * V, &s->buf_gen));
+  if (dump) FH_TRY(ensure(&s->dump, &s->dump_cap, (size_t)B * max_new * V, &s->buf_gen));
   for (int b = 0; b < B; b++)
     HIP_TRY(hipMemcpyAsync(s->tokens + (size_t)b * stride, prompts + (size_t)b * P, sizeof(int32_t) * P,
                            hipMemcpyHostToDevice, st));
   if (uniforms)
     HIP_TRY(hipMemcpyAsync(s->uniforms, uniforms, sizeof(double) * B * max_new, hipMemcpyHostToDevice, st));
   FH_TRY(reset_step_state(s));
-
-  StepPlan plan;
-  plan.P = P;
-  plan.max_new = max_new;
-  plan.tok_stride = stride;
-  plan.opts = opts;
+  g.dump = dump;
+  g.sampled = uniforms != nullptr;
+  g.plan.P = P;
+  g.plan.max_new = max_new;
+  g.plan.tok_stride = stride;
+  g.plan.opts = &g.opts;
   // dump/uniform pointers are baked into the graphs
   float* saved_dump = s->dump;
   double* saved_u = s->uniforms;
-  if (!logits_dump) s->dump = nullptr;
+  if (!dump) s->dump = nullptr;
   if (!uniforms) s->uniforms = nullptr;
   GraphKey key;
   key.B = B;
@@ -1096,71 +1122,147 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   key.dump = s->dump;
   key.uniforms = s->uniforms;
   key.gen = s->buf_gen;
-
   int rc = FH_OK;
-  const int T0 = std::min(P, C);
   // which of steps 1..max_new-1 are cached decode steps (window fits) vs re-prefills
-  int n_dec = 0, n_re = 0;
-  for (int n = 1; n < max_new; n++) (P + n > C ? n_re : n_dec)++;
-  if (s->use_fast() && n_dec > 0 && s->fast.before_launches(n_dec) != FH_OK)
-    return set_err(FH_ERR_HIP, "resetting the fused decode state failed");
-  // greedy on the fused kernel: one launch runs every cached step (the argmax
-  // of a step feeds the next inside the kernel); otherwise one graph per step
-  const bool persistent = n_dec > 0 && fused_greedy(s, opts);
-  if (n_dec > 0 && !persistent) {
+  for (int n = 1; n < max_new; n++) (P + n > C ? g.n_re : g.n_dec)++;
+  if (s->use_fast() && g.n_dec > 0 && s->fast.before_launches(g.n_dec) != FH_OK)
+    rc = set_err(FH_ERR_HIP, "resetting the fused decode state failed");
+  // greedy on the fused kernel: launches run whole runs of cached steps (the
+  // argmax of a step feeds the next inside the kernel); otherwise one graph per step
+  g.persistent = g.n_dec > 0 && fused_greedy(s, opts);
+  if (rc == FH_OK && g.n_dec > 0 && !g.persistent) {
     GraphKey k = key;
     k.kind = 0;
-    rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, plan); });
+    rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, g.plan); });
   }
-  if (rc == FH_OK && n_re > 0) {
+  if (rc == FH_OK && g.n_re > 0) {
     GraphKey k = key;
     k.kind = 1;
-    rc = capture(s, s->g_reprefill, k, [&] { return enqueue_window(s, C, plan); });
-  }
-  if (rc == FH_OK) {
-    (void)hipEventRecord(s->ev[0], st);
-    rc = enqueue_window(s, T0, plan);
-    (void)hipEventRecord(s->ev[1], st);
-    int n = 1;
-    if (rc == FH_OK && persistent) {
-      rc = s->fast.enqueue(st, fused_step(s, plan, 1, n_dec));
-      if (rc != FH_OK) rc = set_err(rc, "fused decode launch failed: %s", hipGetErrorString(hipGetLastError()));
-      n += n_dec;
-    }
-    for (; rc == FH_OK && n < max_new; n++) {
-      hipError_t e = hipGraphLaunch(P + n > C ? s->g_reprefill.exec : s->g_decode.exec, st);
-      if (e != hipSuccess) rc = set_err(FH_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
-    }
-    (void)hipEventRecord(s->ev[2], st);
+    rc = capture(s, s->g_reprefill, k, [&] { return enqueue_window(s, C, g.plan); });
   }
   s->dump = saved_dump;
   s->uniforms = saved_u;
-  if (rc != FH_OK) {
-    (void)hipStreamSynchronize(st);
-    return rc;
+  if (rc != FH_OK) return rc;
+  g.active = true;
+  return FH_OK;
+}
+
+// Enqueues steps gen.next .. upto-1: step 0 is the prompt's window forward,
+// then the cached steps (one fused launch per run of them in greedy mode), then
+// the re-prefill steps once the window slides.
+static int gen_advance(fh_session* s, int upto) {
+  GenState& g = s->gen;
+  hipStream_t st = s->ctx->stream;
+  const int C = s->d.context_length;
+  upto = std::min(upto, g.max_new);
+  float* saved_dump = s->dump;
+  double* saved_u = s->uniforms;
+  if (!g.dump) s->dump = nullptr;
+  if (!g.sampled) s->uniforms = nullptr;
+  int rc = FH_OK;
+  if (g.next == 0 && upto > 0) {
+    rc = enqueue_window(s, std::min(g.P, C), g.plan);
+    g.next = 1;
   }
-  HIP_TRY(hipMemcpyAsync(out_ids, s->out_ids, sizeof(int32_t) * B * max_new, hipMemcpyDeviceToHost, st));
+  while (rc == FH_OK && g.next < upto) {
+    const int n = g.next;
+    if (g.persistent && g.P + n <= C) {
+      const int run = std::min(upto, 1 + g.n_dec) - n;  // cached steps are 1 .. n_dec
+      rc = s->fast.enqueue(st, fused_step(s, g.plan, 1, run));
+      if (rc != FH_OK) rc = set_err(rc, "fused decode launch failed: %s", hipGetErrorString(hipGetLastError()));
+      g.next += run;
+    } else {
+      hipError_t e = hipGraphLaunch(g.P + n > C ? s->g_reprefill.exec : s->g_decode.exec, st);
+      if (e != hipSuccess) rc = set_err(FH_ERR_HIP, "hipGraphLaunch: %s", hipGetErrorString(e));
+      g.next++;
+    }
+  }
+  s->dump = saved_dump;
+  s->uniforms = saved_u;
+  return rc;
+}
+
+// Copies the ids (and logits) produced so far and checks the fused kernel's
+// hand-off status; synchronizes the stream.
+static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
+  GenState& g = s->gen;
+  hipStream_t st = s->ctx->stream;
+  const int B = g.B, V = s->d.vocab_size;
+  HIP_TRY(hipMemcpyAsync(out_ids, s->out_ids, sizeof(int32_t) * B * g.max_new, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipMemcpyAsync(out_counts, s->out_counts, sizeof(int32_t) * B, hipMemcpyDeviceToHost, st));
   if (logits_dump)
-    HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * max_new * V, hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * g.max_new * V, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
   unsigned wait_code = 0;
-  if (s->use_fast() && n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
+  if (s->use_fast() && g.n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
     s->fast.reset();
+    g.active = false;
     return set_err(FH_ERR_HIP,
                    "fused decode step: a hand-off wait exceeded its spin limit (wait %u, layer %u, block %u; "
                    "results discarded)",
                    (wait_code >> 24) & 0x7f, (wait_code >> 16) & 0xff, wait_code & 0xffff);
   }
+  // a sequence without EOS so far has produced every step enqueued
   for (int b = 0; b < B; b++)
-    if (out_counts[b] < 0) out_counts[b] = max_new;
+    if (out_counts[b] < 0) out_counts[b] = g.next;
+  return FH_OK;
+}
+
+int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
+                const double* uniforms, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
+  if (!s || !prompts || !opts || !out_ids || !out_counts) return set_err(FH_ERR_INVALID, "null argument");
+  FH_TRY(gen_setup(s, prompts, batch, P, max_new, opts, uniforms, logits_dump != nullptr));
+  for (int b = 0; b < batch; b++) out_counts[b] = 0;
+  if (max_new == 0) return FH_OK;
+  hipStream_t st = s->ctx->stream;
+  (void)hipEventRecord(s->ev[0], st);
+  int rc = gen_advance(s, 1);
+  (void)hipEventRecord(s->ev[1], st);
+  if (rc == FH_OK) rc = gen_advance(s, max_new);
+  (void)hipEventRecord(s->ev[2], st);
+  if (rc != FH_OK) {
+    s->gen.active = false;
+    (void)hipStreamSynchronize(st);
+    return rc;
+  }
+  FH_TRY(gen_collect(s, out_ids, out_counts, logits_dump));
+  s->gen.active = false;
   float ms0 = 0, ms1 = 0;
   (void)hipEventElapsedTime(&ms0, s->ev[0], s->ev[1]);
   (void)hipEventElapsedTime(&ms1, s->ev[1], s->ev[2]);
   s->t_prefill = ms0;
   s->t_decode = ms1;
-  s->n_cached = n_dec;
-  s->n_reprefill = n_re;
+  s->n_cached = s->gen.n_dec;
+  s->n_reprefill = s->gen.n_re;
+  return FH_OK;
+}
+
+int fh_generate_begin(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
+                      const double* uniforms) {
+  if (!s || !prompts || !opts) return set_err(FH_ERR_INVALID, "null argument");
+  return gen_setup(s, prompts, batch, P, max_new, opts, uniforms, false);
+}
+
+int fh_generate_next(fh_session* s, int steps, int32_t* out_ids, int32_t* out_counts, int32_t* produced) {
+  if (!s || !out_ids || !out_counts || !produced) return set_err(FH_ERR_INVALID, "null argument");
+  if (!s->gen.active) return set_err(FH_ERR_STATE, "no generation in progress (fh_generate_begin first)");
+  if (steps < 1) return set_err(FH_ERR_INVALID, "steps must be positive");
+  GenState& g = s->gen;
+  if (g.max_new == 0) {
+    for (int b = 0; b < g.B; b++) out_counts[b] = 0;
+    *produced = 0;
+    return FH_OK;
+  }
+  HIP_TRY(hipSetDevice(s->ctx->device));
+  int rc = gen_advance(s, g.next + steps);
+  if (rc != FH_OK) {
+    g.active = false;
+    (void)hipStreamSynchronize(s->ctx->stream);
+    return rc;
+  }
+  FH_TRY(gen_collect(s, out_ids, out_counts, nullptr));
+  *produced = g.next;
+  if (g.next >= g.max_new) g.active = false;
   return FH_OK;
 }
 

@@ -32,7 +32,7 @@ EXPORTS = (
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_sample_logits",
-    "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256",
+    "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256", "fh_generate_begin", "fh_generate_next",
 )
 
 
@@ -105,6 +105,8 @@ def lib():
     L.fh_checkpoint_info.argtypes = [ctypes.c_char_p, P(ModelDesc), ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int]
     L.fh_session_load_checkpoint.argtypes = [vp, ctypes.c_char_p]
     L.fh_sha256.argtypes = [vp, ctypes.c_size_t, vp]
+    L.fh_generate_begin.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp]
+    L.fh_generate_next.argtypes = [vp, ctypes.c_int, vp, vp, P(i32)]
     _lib = L
     return L
 

@@ -84,6 +84,55 @@ class Sampler:
         return ids
 
     @staticmethod
+    def generate_stream(model: GptModel, prompt_tokens, max_new_tokens: int, temperature: float, top_k: int,
+                        rng: Optional[Random], eos_id: Optional[int] = None, repetition_penalty: float = 1.0,
+                        no_repeat_ngram_size: int = 0, chunk: int = 16):
+        """Sampler.Generate as the reference's iterator (Sampler.cs:78-109): yields one id
+        at a time for a single prompt, running ``chunk`` device steps per round trip
+        (fh_generate_begin / fh_generate_next).  Stops after yielding ``eos_id``."""
+        if model is None or prompt_tokens is None:
+            raise ValueError("model and prompt_tokens are required")
+        prompt = np.ascontiguousarray(prompt_tokens, np.int32)
+        if prompt.ndim != 1:
+            raise ValueError("generate_stream takes one prompt")
+        if prompt.size == 0:
+            raise ValueError("Need at least one prompt token.")
+        if max_new_tokens < 0:
+            raise ValueError("maxNewTokens must be >= 0")
+        V = model.config.vocab_size
+        if eos_id is not None and not (0 <= eos_id < V):
+            raise ValueError("EOS token must be inside the model vocabulary.")
+        _validate_repetition(repetition_penalty, no_repeat_ngram_size)
+        if not math.isfinite(temperature):
+            raise ValueError("Temperature must be finite.")
+        if chunk < 1:
+            raise ValueError("chunk must be positive")
+        if model.batch != 1:
+            raise ValueError("generate_stream runs a batch-1 session")
+        uniforms = None
+        if temperature > 0:
+            if rng is None:
+                raise ValueError("rng is required when temperature > 0")
+            uniforms = np.ascontiguousarray(rng.next_doubles(max_new_tokens), np.float64)
+        opts = N.Sampling(float(temperature), int(top_k), float(repetition_penalty), int(no_repeat_ngram_size),
+                          -1 if eos_id is None else int(eos_id), 0)
+        N.check(N.lib().fh_generate_begin(model.handle, prompt.ctypes.data, 1, prompt.size, int(max_new_tokens),
+                                          ctypes.byref(opts), None if uniforms is None else uniforms.ctypes.data))
+        out = np.zeros(max(1, max_new_tokens), np.int32)
+        counts = np.zeros(1, np.int32)
+        produced = ctypes.c_int32()
+        yielded = 0
+        while yielded < max_new_tokens:
+            N.check(N.lib().fh_generate_next(model.handle, int(chunk), out.ctypes.data, counts.ctypes.data,
+                                             ctypes.byref(produced)))
+            n = int(counts[0])
+            for i in range(yielded, n):
+                yield int(out[i])
+            yielded = n
+            if n < produced.value or produced.value >= max_new_tokens:  # eos yielded, or done
+                break
+
+    @staticmethod
     def sample_device_logits(backend: HipBackend, logits_dev_ptr, vocab: int, history: Sequence[int],
                              temperature: float, top_k: int, u01: float, repetition_penalty: float = 1.0,
                              no_repeat_ngram_size: int = 0) -> int:

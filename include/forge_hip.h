@@ -157,6 +157,18 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int prompt_len
                 const fh_sampling* opts, const double* uniforms, int32_t* out_ids,
                 int32_t* out_counts, float* logits_dump);
 
+/* Sampler.Generate as a stream (Sampler.cs:78-109 yields one id per step): the same
+ * generation as fh_generate, run a chunk of steps at a time so ids reach the host
+ * (and a tokenizer's decoder) while the loop continues.  fh_generate_begin validates
+ * and uploads like fh_generate and enqueues nothing; each fh_generate_next enqueues up
+ * to `steps` more steps, waits for them, copies out_ids [batch][max_new] and out_counts
+ * as fh_generate does for the steps done so far, and sets *produced to the steps done.
+ * The stream ends after max_new steps; fh_generate, fh_forward_last or a new begin on
+ * the session end it earlier.  The ids equal fh_generate's for any chunking. */
+int fh_generate_begin(fh_session* s, const int32_t* prompts, int batch, int prompt_len, int max_new,
+                      const fh_sampling* opts, const double* uniforms);
+int fh_generate_next(fh_session* s, int steps, int32_t* out_ids, int32_t* out_counts, int32_t* produced);
+
 /* Timing of the last fh_generate, from HIP events on the session stream:
  * prefill_ms (first forward, incl. embedding of the prompt) and decode_ms
  * (all later steps), plus how many decode steps ran without a re-prefill. */

@@ -365,6 +365,38 @@ def test_c5_shape_bf16_window_path_matches_oracle(fhp, oracle, backend, B, P):
             assert ids[b][0] == rids[0]
 
 
+@pytest.mark.parametrize("case", ["greedy_c2", "sampled", "slides", "eos"])
+def test_generate_stream_matches_one_shot(fhp, oracle, backend, case):
+    # Sampler.Generate as an iterator: any chunking of fh_generate_next yields the ids
+    # of one fh_generate call (the fused greedy kernel runs a launch per chunk)
+    if case == "greedy_c2":
+        m = fhp.GptModel(fhp.ModelConfig(16384, 1024, 768, 12, 12), backend, seed=1234)
+        prompt, new, kw = fhp.TrainingRandom(42).ids(16384, 64), 40, {}
+    elif case == "sampled":
+        m = fhp.GptModel(fhp.ModelConfig(2256, 128, 128, 4, 4), backend, seed=1234)
+        prompt, new = fhp.TrainingRandom(42).ids(2256, 16), 30
+        kw = dict(temperature=0.7, top_k=30, repetition_penalty=1.1, no_repeat_ngram_size=4)
+    elif case == "slides":
+        m, oc, w = make_model(fhp, oracle, backend, (32, 8, 16, 2, 2), 8)
+        prompt, new, kw = [1, 2, 3, 4, 5], 12, {}
+    else:
+        m = fhp.GptModel(fhp.ModelConfig(2256, 128, 128, 4, 4), backend, seed=1234)
+        prompt, new = fhp.TrainingRandom(42).ids(2256, 16), 30
+        first = list(fhp.Sampler.generate(m, prompt, new, 0.0, 0, None))
+        kw = dict(eos_id=int(first[9]))
+    T, k = kw.get("temperature", 0.0), kw.get("top_k", 0)
+    extra = {x: kw[x] for x in ("eos_id", "repetition_penalty", "no_repeat_ngram_size") if x in kw}
+    rng = fhp.Random(1) if T > 0 else None
+    want = list(fhp.Sampler.generate(m, prompt, new, T, k, rng, **extra))
+    for chunk in (1, 7, 64):
+        rng = fhp.Random(1) if T > 0 else None
+        got = list(fhp.Sampler.generate_stream(m, prompt, new, T, k, rng, chunk=chunk, **extra))
+        assert got == want, (case, chunk)
+    if case == "eos":
+        assert len(want) <= 10 and want[-1] == kw["eos_id"]
+    m.dispose()
+
+
 def test_c4_shape_batched_decode_matches_oracle(fhp, oracle, backend):
     # Forge-98M shape, 8 sequences decoded together (the batch-32 workload of
     # BASELINE config 4 at a CPU-checkable size): every decode GEMM has M = 8
