@@ -9,3 +9,4 @@ from .model import (BackendSelection, DeviceBuffer, GptModel, HipBackend, ModelC
                     Random, TrainingRandom, get_preset, registry)
 from .sampler import Sampler  # noqa: F401
 from .checkpoint import Checkpoint  # noqa: F401
+from .chat import Chat  # noqa: F401

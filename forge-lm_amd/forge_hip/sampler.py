@@ -59,8 +59,9 @@ class Sampler:
         if temperature > 0:
             if rng is None:
                 raise ValueError("rng is required when temperature > 0")
-            # one NextDouble per sampled step, per sequence (sequence-major)
-            uniforms = np.ascontiguousarray(rng.next_doubles(B * max_new_tokens), np.float64)
+            # one NextDouble per sampled step, per sequence (sequence-major); a single
+            # sequence consumes only the steps it ran (it stops after yielding eos)
+            uniforms = np.ascontiguousarray(rng.peek_doubles(B * max_new_tokens), np.float64)
         opts = N.Sampling(float(temperature), int(top_k), float(repetition_penalty), int(no_repeat_ngram_size),
                           -1 if eos_id is None else int(eos_id), 0)
         out = np.zeros((B, max(1, max_new_tokens)), np.int32)
@@ -75,6 +76,8 @@ class Sampler:
                                        ctypes.byref(nr)))
         Sampler.last_timing = {"prefill_ms": pre.value, "decode_ms": dec.value, "cached_steps": nc.value,
                                "reprefill_steps": nr.value}
+        if uniforms is not None:
+            rng.skip(int(counts[0]) if B == 1 else B * max_new_tokens)
         ids = [out[b, :counts[b]].copy() for b in range(B)]
         if single:
             ids = ids[0]
@@ -113,7 +116,7 @@ class Sampler:
         if temperature > 0:
             if rng is None:
                 raise ValueError("rng is required when temperature > 0")
-            uniforms = np.ascontiguousarray(rng.next_doubles(max_new_tokens), np.float64)
+            uniforms = np.ascontiguousarray(rng.peek_doubles(max_new_tokens), np.float64)
         opts = N.Sampling(float(temperature), int(top_k), float(repetition_penalty), int(no_repeat_ngram_size),
                           -1 if eos_id is None else int(eos_id), 0)
         N.check(N.lib().fh_generate_begin(model.handle, prompt.ctypes.data, 1, prompt.size, int(max_new_tokens),
@@ -122,15 +125,19 @@ class Sampler:
         counts = np.zeros(1, np.int32)
         produced = ctypes.c_int32()
         yielded = 0
-        while yielded < max_new_tokens:
-            N.check(N.lib().fh_generate_next(model.handle, int(chunk), out.ctypes.data, counts.ctypes.data,
-                                             ctypes.byref(produced)))
-            n = int(counts[0])
-            for i in range(yielded, n):
-                yield int(out[i])
-            yielded = n
-            if n < produced.value or produced.value >= max_new_tokens:  # eos yielded, or done
-                break
+        try:
+            while yielded < max_new_tokens:
+                N.check(N.lib().fh_generate_next(model.handle, int(chunk), out.ctypes.data, counts.ctypes.data,
+                                                 ctypes.byref(produced)))
+                n = int(counts[0])
+                for i in range(yielded, n):
+                    yielded = i + 1  # one NextDouble per yielded (sampled) step
+                    yield int(out[i])
+                if n < produced.value or produced.value >= max_new_tokens:  # eos yielded, or done
+                    break
+        finally:
+            if uniforms is not None:
+                rng.skip(yielded)
 
     @staticmethod
     def sample_device_logits(backend: HipBackend, logits_dev_ptr, vocab: int, history: Sequence[int],

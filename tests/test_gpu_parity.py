@@ -397,6 +397,49 @@ def test_generate_stream_matches_one_shot(fhp, oracle, backend, case):
     m.dispose()
 
 
+def test_chat_rolling_context(fhp, oracle, backend):
+    # Program.cs:736-768 on the C1 shape: 6 greedy turns of 60 ids grow the history
+    # past ContextLength (every later turn slides the window) and past 2 x ContextLength
+    # (the history is trimmed); each turn equals the oracle's Generate on the same history
+    shape = (2256, 128, 128, 4, 4)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234)
+    eos = 2255
+    chat = fhp.Chat(m, eos, tokens_per_turn=60, temperature=0.0, chunk=16)
+    hist = [eos]
+    r = fhp.TrainingRandom(5)
+    for turn in range(6):
+        user = [int(t) for t in r.ids(2254, 7)]
+        hist += user
+        hist = hist[-256:]
+        got = list(chat.turn(user))
+        want = [int(t) for t in oracle.generate(oc, w, np.array(hist, np.int32), 60, eos=eos)]
+        assert got == want, turn
+        hist += want
+        assert chat.history == hist
+    chat.reset()
+    assert chat.history == [eos]
+    m.dispose()
+
+
+def test_sampled_generation_consumes_one_uniform_per_step(fhp, backend):
+    # a sampled generation that stops at eos draws one NextDouble per step it ran, so
+    # the next generation on the same Random continues where the reference's would
+    m = fhp.GptModel(fhp.ModelConfig(2256, 128, 128, 4, 4), backend, seed=1234)
+    prompt = fhp.TrainingRandom(42).ids(2256, 16)
+    probe = list(fhp.Sampler.generate(m, prompt, 20, 0.7, 30, fhp.Random(3)))
+    eos = probe[4]
+    n = probe.index(eos) + 1
+    rng = fhp.Random(3)
+    first = list(fhp.Sampler.generate(m, prompt, 20, 0.7, 30, rng, eos_id=eos))
+    assert len(first) == n and rng._pos == n
+    second = list(fhp.Sampler.generate_stream(m, prompt, 20, 0.7, 30, rng, chunk=5))
+    ref = fhp.Random(3)
+    ref.skip(n)
+    assert second == list(fhp.Sampler.generate(m, prompt, 20, 0.7, 30, ref))
+    assert rng._pos == n + 20
+    m.dispose()
+
+
 def test_c4_shape_batched_decode_matches_oracle(fhp, oracle, backend):
     # Forge-98M shape, 8 sequences decoded together (the batch-32 workload of
     # BASELINE config 4 at a CPU-checkable size): every decode GEMM has M = 8
