@@ -185,6 +185,7 @@ struct GenState {
   int next = 0;         // first step not yet enqueued (step 0 is the prompt's forward)
   int n_dec = 0, n_re = 0;
   bool persistent = false, dump = false, sampled = false;
+  bool deferred = false;  // sampled, uniforms supplied per fh_generate_next call
   fh_sampling opts{};
   StepPlan plan;        // plan.opts points at opts
 };
@@ -1060,7 +1061,7 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
 // Validation (Sampler.cs:82-89, 169-175), buffers, prompt upload and the step
 // graphs of a generation; nothing is enqueued yet.  The state lives in s->gen.
 static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
-                     const double* uniforms, bool dump) {
+                     const double* uniforms, bool dump, bool deferred_uniforms = false) {
   s->gen.active = false;
   if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
   if (P <= 0) return set_err(FH_ERR_INVALID, "Need at least one prompt token.");
@@ -1072,7 +1073,7 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   if (opts->no_repeat_ngram < 0) return set_err(FH_ERR_RANGE, "No-repeat n-gram size must be >= 0.");
   if (!std::isfinite(opts->temperature)) return set_err(FH_ERR_INVALID, "Temperature must be finite.");
   if (batch != s->B()) return set_err(FH_ERR_INVALID, "batch %d must equal the session's max_batch %d", batch, s->B());
-  if (opts->temperature > 0.f && !uniforms)
+  if (opts->temperature > 0.f && !uniforms && !deferred_uniforms)
     return set_err(FH_ERR_INVALID, "sampling with temperature > 0 needs one uniform per step");
   FH_TRY(validate_ids(s, prompts, (size_t)batch * P));
   GenState& g = s->gen;
@@ -1091,7 +1092,8 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   const int stride = P + max_new;
   FH_TRY(ensure(&s->tokens, &s->tokens_cap, (size_t)B * stride, &s->buf_gen));
   FH_TRY(ensure(&s->out_ids, &s->out_cap, (size_t)B * max_new, &s->buf_gen));
-  if (uniforms) FH_TRY(ensure(&s->uniforms, &s->uni_cap, (size_t)B * max_new, &s->buf_gen));
+  const bool sampled = opts->temperature > 0.f;
+  if (sampled) FH_TRY(ensure(&s->uniforms, &s->uni_cap, (size_t)B * max_new, &s->buf_gen));
   if (dump) FH_TRY(ensure(&s->dump, &s->dump_cap, (size_t)B * max_new * V, &s->buf_gen));
   for (int b = 0; b < B; b++)
     HIP_TRY(hipMemcpyAsync(s->tokens + (size_t)b * stride, prompts + (size_t)b * P, sizeof(int32_t) * P,
@@ -1100,7 +1102,8 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
     HIP_TRY(hipMemcpyAsync(s->uniforms, uniforms, sizeof(double) * B * max_new, hipMemcpyHostToDevice, st));
   FH_TRY(reset_step_state(s));
   g.dump = dump;
-  g.sampled = uniforms != nullptr;
+  g.sampled = sampled;
+  g.deferred = sampled && !uniforms;
   g.plan.P = P;
   g.plan.max_new = max_new;
   g.plan.tok_stride = stride;
@@ -1109,7 +1112,7 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   float* saved_dump = s->dump;
   double* saved_u = s->uniforms;
   if (!dump) s->dump = nullptr;
-  if (!uniforms) s->uniforms = nullptr;
+  if (!sampled) s->uniforms = nullptr;
   GraphKey key;
   key.B = B;
   key.P = P;
@@ -1240,10 +1243,11 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
 int fh_generate_begin(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
                       const double* uniforms) {
   if (!s || !prompts || !opts) return set_err(FH_ERR_INVALID, "null argument");
-  return gen_setup(s, prompts, batch, P, max_new, opts, uniforms, false);
+  return gen_setup(s, prompts, batch, P, max_new, opts, uniforms, false, true);
 }
 
-int fh_generate_next(fh_session* s, int steps, int32_t* out_ids, int32_t* out_counts, int32_t* produced) {
+int fh_generate_next(fh_session* s, int steps, const double* uniforms, int32_t* out_ids, int32_t* out_counts,
+                     int32_t* produced) {
   if (!s || !out_ids || !out_counts || !produced) return set_err(FH_ERR_INVALID, "null argument");
   if (!s->gen.active) return set_err(FH_ERR_STATE, "no generation in progress (fh_generate_begin first)");
   if (steps < 1) return set_err(FH_ERR_INVALID, "steps must be positive");
@@ -1254,6 +1258,14 @@ int fh_generate_next(fh_session* s, int steps, int32_t* out_ids, int32_t* out_co
     return FH_OK;
   }
   HIP_TRY(hipSetDevice(s->ctx->device));
+  const int n = std::min(steps, g.max_new - g.next);
+  if (g.deferred) {
+    // this call's uniforms, [batch][steps], for steps next .. next+n-1
+    if (!uniforms) return set_err(FH_ERR_INVALID, "sampling with temperature > 0 needs one uniform per step");
+    for (int b = 0; b < g.B; b++)
+      HIP_TRY(hipMemcpyAsync(s->uniforms + (size_t)b * g.max_new + g.next, uniforms + (size_t)b * steps,
+                             sizeof(double) * n, hipMemcpyHostToDevice, s->ctx->stream));
+  }
   int rc = gen_advance(s, g.next + steps);
   if (rc != FH_OK) {
     g.active = false;

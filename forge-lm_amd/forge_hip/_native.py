@@ -106,7 +106,7 @@ def lib():
     L.fh_session_load_checkpoint.argtypes = [vp, ctypes.c_char_p]
     L.fh_sha256.argtypes = [vp, ctypes.c_size_t, vp]
     L.fh_generate_begin.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp]
-    L.fh_generate_next.argtypes = [vp, ctypes.c_int, vp, vp, P(i32)]
+    L.fh_generate_next.argtypes = [vp, ctypes.c_int, vp, vp, vp, P(i32)]
     _lib = L
     return L
 

@@ -127,8 +127,8 @@ class Sampler:
         yielded = 0
         try:
             while yielded < max_new_tokens:
-                N.check(N.lib().fh_generate_next(model.handle, int(chunk), out.ctypes.data, counts.ctypes.data,
-                                                 ctypes.byref(produced)))
+                N.check(N.lib().fh_generate_next(model.handle, int(chunk), None, out.ctypes.data,
+                                                 counts.ctypes.data, ctypes.byref(produced)))
                 n = int(counts[0])
                 for i in range(yielded, n):
                     yielded = i + 1  # one NextDouble per yielded (sampled) step

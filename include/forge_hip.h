@@ -163,11 +163,15 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int prompt_len
  * and uploads like fh_generate and enqueues nothing; each fh_generate_next enqueues up
  * to `steps` more steps, waits for them, copies out_ids [batch][max_new] and out_counts
  * as fh_generate does for the steps done so far, and sets *produced to the steps done.
- * The stream ends after max_new steps; fh_generate, fh_forward_last or a new begin on
- * the session end it earlier.  The ids equal fh_generate's for any chunking. */
+ * Sampled generations take the uniforms either all at begin ([batch][max_new]) or, when
+ * begin's uniforms are null, per call ([batch][steps], one NextDouble per step, so a
+ * caller that stops after eos has drawn exactly the reference's count).  The stream ends
+ * after max_new steps; fh_generate, fh_forward_last or a new begin on the session end it
+ * earlier.  The ids equal fh_generate's for any chunking. */
 int fh_generate_begin(fh_session* s, const int32_t* prompts, int batch, int prompt_len, int max_new,
                       const fh_sampling* opts, const double* uniforms);
-int fh_generate_next(fh_session* s, int steps, int32_t* out_ids, int32_t* out_counts, int32_t* produced);
+int fh_generate_next(fh_session* s, int steps, const double* uniforms, int32_t* out_ids, int32_t* out_counts,
+                     int32_t* produced);
 
 /* Timing of the last fh_generate, from HIP events on the session stream:
  * prefill_ms (first forward, incl. embedding of the prompt) and decode_ms

@@ -397,6 +397,37 @@ def test_generate_stream_matches_one_shot(fhp, oracle, backend, case):
     m.dispose()
 
 
+def test_stream_with_uniforms_per_call(fhp, backend):
+    # fh_generate_begin without uniforms: each fh_generate_next brings its chunk's
+    # uniforms, as a caller drawing NextDouble per step would (C3 options)
+    import ctypes
+    N = fhp._native
+    m = fhp.GptModel(fhp.ModelConfig(2256, 128, 128, 4, 4), backend, seed=1234)
+    prompt = np.ascontiguousarray(fhp.TrainingRandom(42).ids(2256, 16), np.int32)
+    new = 23
+    want = list(fhp.Sampler.generate(m, prompt, new, 0.7, 30, fhp.Random(1), repetition_penalty=1.1,
+                                     no_repeat_ngram_size=4))
+    u = fhp.Random(1).next_doubles(new)
+    opts = N.Sampling(0.7, 30, 1.1, 4, -1, 0)
+    N.check(N.lib().fh_generate_begin(m.handle, prompt.ctypes.data, 1, prompt.size, new, ctypes.byref(opts), None))
+    out = np.zeros(new, np.int32)
+    counts = np.zeros(1, np.int32)
+    produced = ctypes.c_int32()
+    done = 0
+    while done < new:
+        chunk = np.ascontiguousarray(u[done:done + 5])
+        buf = np.zeros(5, np.float64)
+        buf[:chunk.size] = chunk
+        N.check(N.lib().fh_generate_next(m.handle, 5, buf.ctypes.data, out.ctypes.data, counts.ctypes.data,
+                                         ctypes.byref(produced)))
+        done = produced.value
+    assert list(out[:counts[0]]) == want
+    with pytest.raises(fhp.HipError):
+        N.check(N.lib().fh_generate_next(m.handle, 1, None, out.ctypes.data, counts.ctypes.data,
+                                         ctypes.byref(produced)))  # the stream has ended
+    m.dispose()
+
+
 def test_chat_rolling_context(fhp, oracle, backend):
     # Program.cs:736-768 on the C1 shape: 6 greedy turns of 60 ids grow the history
     # past ContextLength (every later turn slides the window) and past 2 x ContextLength
