@@ -320,6 +320,28 @@ int linear(fh_session* s, const float* x, int M, int K, size_t slot, int N, cons
   return FH_OK;
 }
 
+// x @ W for registry matrix `slot` into split-K partials s->part (no bias or
+// epilogue); *S receives the split count for the fused epilogue that sums them.
+template <typename WT>
+int linear_parts(fh_session* s, const float* x, int M, int K, size_t slot, int N, int* S) {
+  hipStream_t st = s->ctx->stream;
+  if (M <= 4) {
+    const int splits = std::max(1, std::min(64, K / 16));
+    LAUNCH(launch_gemv_splitk<WT>(st, x, M, K, s->w<WT>(slot), N, s->part, splits, S));
+  } else {
+    LAUNCH(launch_gemm_mfma_split<WT>(st, x, M, K, s->wt<WT>(slot), N, s->part, s->part_floats,
+                                      s->ctx->props.multiProcessorCount, S));
+  }
+  return FH_OK;
+}
+
+// Whether a decode step folds the split-K reductions into the kernels after them
+// (qkv + KV store, proj + LN2, mproj + the next LayerNorm, LN_f included).
+bool decode_fused_epilogues(const fh_session* s) {
+  const int D = s->d.d_model;
+  return D <= 1024 && (s->B() <= 4 || D % 32 == 0);
+}
+
 // Tied head for B rows: logits = xn @ tok_emb^T.  tok_emb [V][d] is already
 // the transposed operand the MFMA GEMM reads, so more than 4 rows go there.
 template <typename WT>
@@ -398,6 +420,33 @@ template <typename WT>
 int enqueue_layers_decode(fh_session* s, RowSrc src) {
   hipStream_t st = s->ctx->stream;
   const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length;
+  if (decode_fused_epilogues(s)) {
+    // each split-K reduction also does the work of the kernel after it; the last
+    // mproj reduction applies LN_f, so xn holds the head's input on return
+    const int L = s->d.n_layers;
+    LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
+    for (int l = 0; l < L; l++) {
+      WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+      WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+      int S = 0;
+      FH_TRY(linear_parts<WT>(s, s->xn, B, D, s->idx_blk(l, 2), 3 * D, &S));
+      LAUNCH(launch_epilogue_qkv<WT>(st, s->part, S, B, D, s->v(s->idx_blk(l, 3)), s->qkv, src, 1, H, C, kc, vc));
+      if (D == 64 * H)
+        LAUNCH(launch_attn_decode_wide<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, s->o));
+      else
+        LAUNCH(launch_attn_decode<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, 64, s->o));
+      FH_TRY(linear_parts<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, &S));
+      LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 5)), s->x, s->x2, s->v(s->idx_blk(l, 6)),
+                                s->v(s->idx_blk(l, 7)), s->xn, 1e-5f));
+      FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+                        s->h));
+      FH_TRY(linear_parts<WT>(s, s->h, B, 4 * D, s->idx_blk(l, 10), D, &S));
+      const size_t ln = l + 1 < L ? s->idx_blk(l + 1, 0) : s->idx_lnf();
+      LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 11)), s->x2, s->x, s->v(ln), s->v(ln + 1),
+                                s->xn, 1e-5f));
+    }
+    return FH_OK;
+  }
   for (int l = 0; l < s->d.n_layers; l++) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
@@ -505,7 +554,8 @@ int enqueue_decode_step(fh_session* s, const StepPlan& p) {
                             s->d.context_length, s->x));
     FH_TRY(enqueue_layers_decode<WT>(s, src));
     const size_t lf = s->idx_lnf();
-    LAUNCH(launch_layernorm(st, s->x, B, 1, 1, 0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
+    if (!decode_fused_epilogues(s))
+      LAUNCH(launch_layernorm(st, s->x, B, 1, 1, 0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
     FH_TRY(head<WT>(s, B));
   }
   LAUNCH(launch_sample(st, make_sample_args(s, p)));

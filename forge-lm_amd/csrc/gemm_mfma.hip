@@ -283,6 +283,34 @@ hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const 
   return launch_splitk_epilogue(st, part, S, M, N, bias, epi, res, y);
 }
 
+template <typename WT>
+hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, float* part,
+                                  size_t part_floats, int cus, int* splits) {
+  if (!a || !Wt || !part || !splits || M <= 0 || N <= 0 || K <= 0 || K % BK != 0 || (size_t)M * N > part_floats)
+    return hipErrorInvalidValue;
+  if ((size_t)128 * K * 4 > 0x7fffffffu) return hipErrorInvalidValue;
+  const int gn = (N + BN - 1) / BN;
+  const int bm = M > 64 ? 128 : (M > 32 ? 64 : 32);
+  const int gm = (M + bm - 1) / bm;
+  int S = 1;
+  const int target = 2 * (cus > 0 ? cus : 256);
+  while (gn * gm * S * 2 <= target && (K / BK) % (S * 2) == 0 && (size_t)S * 2 * M * N <= part_floats) S *= 2;
+  *splits = S;
+  const int kchunk = K / S;
+  dim3 grid(gn, gm, S);
+  const bool resident = kchunk <= 3 * BK;
+  if (bm == 128) return launch_epi<WT, 128, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
+  if (bm == 64)
+    return resident ? launch_epi<WT, 64, 3>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part)
+                    : launch_epi<WT, 64, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
+  return resident ? launch_epi<WT, 32, 3>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part)
+                  : launch_epi<WT, 32, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
+}
+
+template hipError_t launch_gemm_mfma_split<float>(hipStream_t, const float*, int, int, const float*, int, float*,
+                                                  size_t, int, int*);
+template hipError_t launch_gemm_mfma_split<bf16_t>(hipStream_t, const float*, int, int, const bf16_t*, int, float*,
+                                                   size_t, int, int*);
 template hipError_t launch_transpose<float>(hipStream_t, const float*, int, int, float*);
 template hipError_t launch_transpose<bf16_t>(hipStream_t, const bf16_t*, int, int, bf16_t*);
 template hipError_t launch_gemm_mfma<float>(hipStream_t, const float*, int, int, const float*, int, const float*, int,

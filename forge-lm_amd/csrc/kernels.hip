@@ -152,6 +152,103 @@ __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __rest
   }
 }
 
+// Split-K reduction (k_splitk_epilogue's sum, bias, residual) fused with the
+// LayerNorm that follows: one block per row writes the row to y and its
+// LayerNorm to out, with k_layernorm's per-thread columns and reductions, so
+// both outputs equal the two separate kernels' bit for bit.  N <= 1024.
+__global__ __launch_bounds__(256) void k_epilogue_ln(const float* __restrict__ part, int S, int M, int N,
+                                                     const float* __restrict__ bias, const float* __restrict__ res,
+                                                     float* __restrict__ y, const float* __restrict__ w,
+                                                     const float* __restrict__ b, float* __restrict__ out,
+                                                     float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  // partials through a bounded resource: 8 partials of the thread's 4 columns in
+  // flight together, skipped ones (past S or N) read as zeros; each column sums
+  // its partials in order, and the zeros after the last one change nothing
+  const int pbytes = (int)((size_t)S * M * N * 4);
+  const __amdgpu_buffer_rsrc_t rp =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part), (short)0, pbytes, 0x00020000);
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < S; i0 += 8) {
+    float t[8][4];
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int c = threadIdx.x + 256 * q;
+        const int off =
+            (c < N && i0 + ii < S) ? (int)((((size_t)(i0 + ii) * M + r) * N + c) * 4) : pbytes;
+        t[ii][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
+      }
+#pragma unroll
+    for (int ii = 0; ii < 8; ii++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) v[q] += t[ii][q];
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int c = threadIdx.x + 256 * q;
+    if (c < N) {
+      const size_t idx = (size_t)r * N + c;
+      float a = v[q];
+      if (bias) a += bias[c];
+      if (res) a += res[idx];
+      y[idx] = a;
+      v[q] = a;
+      s += a;
+    } else {
+      v[q] = 0.f;
+    }
+  }
+  const float mu = block_sum<256>(s, red) / (float)N;
+  float var = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int c = threadIdx.x + 256 * q;
+    if (c < N) {
+      const float dd = v[q] - mu;
+      var += dd * dd;
+    }
+  }
+  const float vs = block_sum<256>(var, red);
+  const float rs = 1.f / sqrtf(vs / (float)N + eps);
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    const int c = threadIdx.x + 256 * q;
+    if (c < N) out[(size_t)r * N + c] = (v[q] - mu) * rs * w[c] + b[c];
+  }
+}
+
+// Split-K reduction of a qkv projection (sum + bias into qkv) fused with the KV
+// store: the K and V columns also go to the caches at the row's position, as
+// k_kv_store writes them.
+template <typename KT>
+__global__ __launch_bounds__(256) void k_epilogue_qkv(const float* __restrict__ part, int S, int M, int d,
+                                                      const float* __restrict__ bias, float* __restrict__ qkv,
+                                                      RowSrc src, int T, int H, int ctx, KT* __restrict__ kc,
+                                                      KT* __restrict__ vc) {
+  const int N = 3 * d;
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)M * N) return;
+  const int col = (int)(idx % N), r = (int)(idx / N);
+  float a = 0.f;
+#pragma unroll 8
+  for (int i = 0; i < S; i++) a += part[(size_t)i * M * N + idx];
+  if (bias) a += bias[col];
+  qkv[idx] = a;
+  if (col < d) return;
+  const int pos = src.pos_off + src.pos_mul * *src.step + r % T;
+  if ((unsigned)pos >= (unsigned)ctx) return;
+  const int hd = d / H, c = col < 2 * d ? col - d : col - 2 * d, h = c / hd, e = c % hd;
+  const size_t dst = (((size_t)(r / T) * H + h) * ctx + pos) * hd + e;
+  if (col < 2 * d)
+    kc[dst] = from_f32<KT>(a);
+  else
+    vc[dst] = from_f32<KT>(a);
+}
+
 // ---------------------------------------------------------------------------
 // split-K GEMV (M <= 4): each block owns a 64*VEC column tile and one K chunk;
 // each of its 4 waves walks every 4th row of the chunk with 16-byte loads.
@@ -1366,6 +1463,29 @@ hipError_t launch_head(hipStream_t st, const float* xn, int B, int d, const WT* 
   hipLaunchKernelGGL(k_head<WT>, dim3(blocks), dim3(256), 0, st, xn, B, d, E, V, logits);
   return hipGetLastError();
 }
+
+hipError_t launch_epilogue_ln(hipStream_t st, const float* part, int splits, int M, int N, const float* bias,
+                              const float* res, float* y, const float* w, const float* b, float* out, float eps) {
+  FH_CHECK_ARG(splits >= 1 && M > 0 && N > 0 && N <= 1024 && part && y && w && b && out &&
+               (size_t)splits * M * N * 4 < 0x7fffffffu);
+  hipLaunchKernelGGL(k_epilogue_ln, dim3(M), dim3(256), 0, st, part, splits, M, N, bias, res, y, w, b, out, eps);
+  return hipGetLastError();
+}
+
+template <typename KT>
+hipError_t launch_epilogue_qkv(hipStream_t st, const float* part, int splits, int M, int d, const float* bias,
+                               float* qkv, RowSrc src, int T, int H, int ctx, KT* kcache, KT* vcache) {
+  FH_CHECK_ARG(splits >= 1 && M > 0 && d > 0 && H > 0 && d % H == 0 && T > 0 && M % T == 0 && ctx > 0 && part &&
+               qkv && kcache && vcache && src.step);
+  const size_t tot = (size_t)M * 3 * d;
+  hipLaunchKernelGGL(k_epilogue_qkv<KT>, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st, part, splits, M, d,
+                     bias, qkv, src, T, H, ctx, kcache, vcache);
+  return hipGetLastError();
+}
+template hipError_t launch_epilogue_qkv<float>(hipStream_t, const float*, int, int, int, const float*, float*, RowSrc,
+                                               int, int, int, float*, float*);
+template hipError_t launch_epilogue_qkv<bf16_t>(hipStream_t, const float*, int, int, int, const float*, float*,
+                                                RowSrc, int, int, int, bf16_t*, bf16_t*);
 
 hipError_t launch_round_bf16(hipStream_t st, const float* in, size_t n, bf16_t* out) {
   FH_CHECK_ARG(in && out);

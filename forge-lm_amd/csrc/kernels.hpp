@@ -32,6 +32,18 @@ hipError_t launch_gemv_splitk(hipStream_t st, const float* x, int M, int K, cons
 hipError_t launch_splitk_epilogue(hipStream_t st, const float* part, int splits, int M, int N, const float* bias,
                                   int epi, const float* res, float* y);
 
+// The split-K reduction fused with the LayerNorm that follows (N <= 1024): y = sum_s
+// part[s] + bias (+ res), out = LN(y) per row; equal to launch_splitk_epilogue then
+// launch_layernorm.
+hipError_t launch_epilogue_ln(hipStream_t st, const float* part, int splits, int M, int N, const float* bias,
+                              const float* res, float* y, const float* w, const float* b, float* out, float eps);
+
+// The split-K reduction of a qkv projection fused with the KV store: qkv = sum_s
+// part[s] + bias, and the K, V columns into the caches at pos(row) (as launch_kv_store).
+template <typename KT>
+hipError_t launch_epilogue_qkv(hipStream_t st, const float* part, int splits, int M, int d, const float* bias,
+                               float* qkv, RowSrc src, int T, int H, int ctx, KT* kcache, KT* vcache);
+
 // Tiled GEMM for any M: y[m,n] = epi(sum_k a[m,k] W[k,n] + bias[n]) (+ res[m,n]).
 template <typename WT>
 hipError_t launch_gemm(hipStream_t st, const float* a, int M, int K, const WT* W, int N, const float* bias, int epi,
@@ -110,6 +122,12 @@ struct GemmBf16Out {
 // row's position (rows past ctx are dropped), D = 64 H.
 hipError_t launch_gemm_bf16_qkv(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, const float* bias,
                                 RowSrc src, int T, int H, int ctx, bf16_t* q, bf16_t* kcache, bf16_t* vcache);
+
+// The same GEMM writing only the split-K partials part[S][M][N] (S >= 1, returned
+// in *splits) for a fused epilogue to reduce.
+template <typename WT>
+hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, float* part,
+                                  size_t part_floats, int cus, int* splits);
 
 // Wt[n][k] = W[k][n].
 template <typename WT>

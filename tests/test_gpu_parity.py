@@ -533,3 +533,29 @@ def test_batched_decode_attention_over_several_chunks(fhp, oracle, backend):
         np.testing.assert_array_equal(ids[b], rids)
         assert rel_err(lg[b], rlg) <= TOL_F32
     m.dispose()
+
+
+@pytest.mark.parametrize("B,dtype", [(33, "f32"), (70, "f32"), (12, "bf16")])
+def test_batched_decode_fused_epilogues(fhp, oracle, backend, B, dtype):
+    # batched decode sums the split-K partials in kernels that also do the next
+    # step (qkv + KV store, proj + LN2, mlp.proj + the next LayerNorm or LN_f):
+    # 33 and 70 rows take the GEMM's 64- and 128-row tiles
+    shape = (512, 64, 128, 2, 2)
+    ocfg = oracle.Config(*shape)
+    w = oracle.init_weights(ocfg, 5)
+    wref = bf16_round(w)[0] if dtype == "bf16" else w
+    tol = 2e-2 if dtype == "bf16" else TOL_F32
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype=dtype)
+    m.load_weights(w)
+    r = fhp.TrainingRandom(17)
+    prompts = np.stack([r.ids(shape[0], 10) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, 8, 0.0, 0, None, return_logits=True)
+    for b in range(B):
+        rids, rlg = oracle.generate(ocfg, wref, prompts[b], 8, return_logits=True)
+        top2 = np.sort(rlg, axis=1)[:, -2:]
+        for n in range(8):
+            assert rel_err(lg[b][n], rlg[n]) <= tol, (b, n)
+            if top2[n, 1] - top2[n, 0] <= 2 * tol:  # a near tie may flip; later steps then differ
+                break
+            assert ids[b][n] == rids[n], (b, n)
+    m.dispose()
