@@ -63,6 +63,16 @@ static int set_err(int code, const char* fmt, ...) {
   return code;
 }
 
+namespace fh {
+// the same thread-local message, for the op entry points (ops.hip)
+int set_error(int code, const char* msg) {
+  g_err = msg;
+  return code;
+}
+struct OpsState;
+void ops_state_free(OpsState* o);
+}  // namespace fh
+
 #define HIP_TRY(expr)                                                                                   \
   do {                                                                                                  \
     hipError_t e_ = (expr);                                                                             \
@@ -148,7 +158,14 @@ struct fh_context {
   double* s_u = nullptr;
   int sessions = 0;              // live sessions on this context
   bool destroy_pending = false;  // fh_context_destroy ran while sessions were alive
+  fh::OpsState* ops = nullptr;   // state of the op-level entry points (ops.hip)
 };
+
+namespace fh {
+hipStream_t context_stream(fh_context* c) { return c->stream; }
+int context_device(fh_context* c) { return c->device; }
+OpsState*& context_ops(fh_context* c) { return c->ops; }
+}  // namespace fh
 
 // ---------------------------------------------------------------------------
 // session
@@ -706,6 +723,7 @@ static void context_free(fh_context* c) {
   dev_free(c->s_work);
   dev_free(c->s_ints);
   dev_free(c->s_u);
+  ops_state_free(c->ops);
   if (c->stream) (void)hipStreamDestroy(c->stream);
   delete c;
 }

@@ -33,6 +33,15 @@ EXPORTS = (
     "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_sample_logits",
     "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256", "fh_generate_begin", "fh_generate_next",
+    # op-level ITensorBackend
+    "fh_op_matmul_nn", "fh_op_matmul_nt", "fh_op_matmul_tn", "fh_op_pack_heads", "fh_op_unpack_heads",
+    "fh_op_add_bias", "fh_op_sum_rows", "fh_op_add_in_place", "fh_op_copy", "fh_op_scale", "fh_op_zero",
+    "fh_op_copy_block", "fh_op_transpose", "fh_op_layernorm_forward", "fh_op_layernorm_backward",
+    "fh_op_softmax_forward", "fh_op_scaled_causal_softmax_forward", "fh_op_softmax_backward",
+    "fh_op_gelu_forward", "fh_op_gelu_backward", "fh_op_embedding_forward", "fh_op_embedding_backward",
+    "fh_op_causal_mask", "fh_op_cross_entropy_forward", "fh_op_begin_loss_accumulation",
+    "fh_op_end_loss_accumulation", "fh_op_cross_entropy_backward", "fh_op_sum_squares",
+    "fh_op_global_sum_squares", "fh_op_adamw_step",
 )
 
 
@@ -62,6 +71,10 @@ class ArgumentError(HipError, ValueError):
 
 class InvalidDataError(HipError, ValueError):
     """FH_ERR_DATA: the reference's InvalidDataException (malformed or corrupted checkpoint)."""
+
+
+class InvalidOperationError(HipError):
+    """FH_ERR_STATE: the reference's InvalidOperationException (a call out of order)."""
 
 
 _lib = None
@@ -107,6 +120,36 @@ def lib():
     L.fh_sha256.argtypes = [vp, ctypes.c_size_t, vp]
     L.fh_generate_begin.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp]
     L.fh_generate_next.argtypes = [vp, ctypes.c_int, vp, vp, vp, P(i32)]
+    ci, cf = ctypes.c_int, ctypes.c_float
+    for mm in ("nn", "nt", "tn"):
+        getattr(L, f"fh_op_matmul_{mm}").argtypes = [vp, vp, vp, vp, ci, ci, ci, ci, ci]
+    L.fh_op_pack_heads.argtypes = [vp, vp, ci, vp, ci, ci, ci, ci, ci]
+    L.fh_op_unpack_heads.argtypes = [vp, vp, vp, ci, ci, ci, ci, ci, ci]
+    L.fh_op_add_bias.argtypes = [vp, vp, vp, ci, ci]
+    L.fh_op_sum_rows.argtypes = [vp, vp, vp, ci, ci]
+    L.fh_op_add_in_place.argtypes = [vp, vp, vp, i64]
+    L.fh_op_copy.argtypes = [vp, vp, vp, i64]
+    L.fh_op_scale.argtypes = [vp, vp, i64, cf]
+    L.fh_op_zero.argtypes = [vp, vp, i64]
+    L.fh_op_copy_block.argtypes = [vp, vp, ci, vp, ci, ci, ci, ci, ci, ci, ci]
+    L.fh_op_transpose.argtypes = [vp, vp, vp, ci, ci]
+    L.fh_op_layernorm_forward.argtypes = [vp, vp, vp, vp, vp, vp, vp, ci, ci, cf]
+    L.fh_op_layernorm_backward.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp, ci, ci]
+    L.fh_op_softmax_forward.argtypes = [vp, vp, ci, ci]
+    L.fh_op_scaled_causal_softmax_forward.argtypes = [vp, vp, ci, ci, cf]
+    L.fh_op_softmax_backward.argtypes = [vp, vp, vp, vp, ci, ci, cf]
+    L.fh_op_gelu_forward.argtypes = [vp, vp, vp, i64]
+    L.fh_op_gelu_backward.argtypes = [vp, vp, vp, vp, i64]
+    L.fh_op_embedding_forward.argtypes = [vp, vp, ci, vp, ci, vp, ci]
+    L.fh_op_embedding_backward.argtypes = [vp, vp, vp, ci, vp, ci, ci]
+    L.fh_op_causal_mask.argtypes = [vp, vp, i64, ci]
+    L.fh_op_cross_entropy_forward.argtypes = [vp, vp, vp, vp, ci, ci, ci, P(f32)]
+    L.fh_op_begin_loss_accumulation.argtypes = [vp]
+    L.fh_op_end_loss_accumulation.argtypes = [vp, P(f32)]
+    L.fh_op_cross_entropy_backward.argtypes = [vp, vp, vp, vp, ci, ci, ci]
+    L.fh_op_sum_squares.argtypes = [vp, vp, i64, P(f64)]
+    L.fh_op_global_sum_squares.argtypes = [vp, P(vp), P(i64), ci, P(f64)]
+    L.fh_op_adamw_step.argtypes = [vp, vp, vp, vp, vp, i64, cf, cf, cf, cf, cf, ci, ci]
     _lib = L
     return L
 
@@ -126,4 +169,6 @@ def check(code: int) -> int:
         raise ArgumentError(code, msg)
     if code == FH_ERR_DATA:
         raise InvalidDataError(code, msg)
+    if code == FH_ERR_STATE:
+        raise InvalidOperationError(code, msg)
     raise HipError(code, msg)

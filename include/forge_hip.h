@@ -185,6 +185,91 @@ int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t
 int fh_sample_logits(fh_context* ctx, const float* logits_dev, int V, const int32_t* history,
                      int n_hist, const fh_sampling* opts, double u01, int32_t* out_id);
 
+/* ---- op-level ITensorBackend on device buffers ---------------------------------
+ * One entry point per ITensorBackend method (src/LLM.Core/Tensor/ITensorBackend.cs);
+ * every tensor argument is a device pointer to row-major fp32 of the documented
+ * shape, sizes are explicit.  Work is ordered on the context's stream and returns
+ * without waiting, except where a host value comes back (the cross-entropy loss,
+ * fh_op_end_loss_accumulation, the sums of squares) or a host index array is
+ * uploaded (it is copied before the call returns).  `accumulate` means += into y.
+ * The host mirror keeps the residency contract (InvalidateDeviceCache /
+ * EnsureHostCurrent, ITensorBackend.cs:166-193) over these pointers. */
+
+/* MatMulNN / BatchedMatMulNN (ITensorBackend.cs:22, 35): per slot s < slots,
+ * y[s] (+)= a[s] @ b[s]; a [slots*M, K], b [slots*K, N], y [slots*M, N]. */
+int fh_op_matmul_nn(fh_context* ctx, const void* a, const void* b, void* y, int slots, int M, int K, int N,
+                    int accumulate);
+/* MatMulNT / BatchedMatMulNT (:24, 37): y[s] (+)= a[s] @ b[s]^T; b [slots*N, K]. */
+int fh_op_matmul_nt(fh_context* ctx, const void* a, const void* b, void* y, int slots, int M, int K, int N,
+                    int accumulate);
+/* MatMulTN / BatchedMatMulTN (:26, 39): y[s] (+)= a[s]^T @ b[s]; a [slots*K, M]. */
+int fh_op_matmul_tn(fh_context* ctx, const void* a, const void* b, void* y, int slots, int M, int K, int N,
+                    int accumulate);
+/* PackHeads (:49): dst[(q*H+h)*T+t, e] = src[q*T+t, col_base+h*hd+e]; src rows are
+ * src_cols wide.  UnpackHeads (:55) is the inverse into dst rows dst_cols wide. */
+int fh_op_pack_heads(fh_context* ctx, const void* src, int src_cols, void* dst, int batch, int T, int n_heads,
+                     int head_dim, int col_base);
+int fh_op_unpack_heads(fh_context* ctx, const void* src, void* dst, int dst_cols, int batch, int T, int n_heads,
+                       int head_dim, int col_base);
+/* AddBias (:80) y[r,:] += bias; SumRows (:82) dbias += column sums of dy (accumulates). */
+int fh_op_add_bias(fh_context* ctx, void* y, const void* bias, int rows, int cols);
+int fh_op_sum_rows(fh_context* ctx, const void* dy, void* dbias, int rows, int cols);
+/* AddInPlace (:84), Copy (:86), Scale (:94), Zero (:200) over n floats. */
+int fh_op_add_in_place(fh_context* ctx, void* dst, const void* src, int64_t n);
+int fh_op_copy(fh_context* ctx, const void* src, void* dst, int64_t n);
+int fh_op_scale(fh_context* ctx, void* x, int64_t n, float factor);
+int fh_op_zero(fh_context* ctx, void* x, int64_t n);
+/* CopyBlock (:92): rows x cols block from (src_row, src_col) of src to (dst_row,
+ * dst_col) of dst; the rest of dst is kept. */
+int fh_op_copy_block(fh_context* ctx, const void* src, int src_cols, void* dst, int dst_cols, int src_row,
+                     int src_col, int dst_row, int dst_col, int rows, int cols);
+/* Transpose (:96): out [cols, rows] = x [rows, cols]^T. */
+int fh_op_transpose(fh_context* ctx, const void* x, void* out, int rows, int cols);
+/* LayerNormForward (:103): out, and mean / rstd [rows]; LayerNormBackward (:106): dx
+ * overwritten, dw and db accumulate. */
+int fh_op_layernorm_forward(fh_context* ctx, const void* x, const void* w, const void* b, void* out, void* mean,
+                            void* rstd, int rows, int cols, float eps);
+int fh_op_layernorm_backward(fh_context* ctx, const void* dout, const void* x, const void* w, const void* mean,
+                             const void* rstd, void* dx, void* dw, void* db, int rows, int cols);
+/* SoftmaxForward (:112) in place; ScaledCausalSoftmaxForward (:117): scale, causal mask
+ * (row r is query r % T of a packed [T,T] block) and softmax, in place. */
+int fh_op_softmax_forward(fh_context* ctx, void* x, int rows, int cols);
+int fh_op_scaled_causal_softmax_forward(fh_context* ctx, void* scores, int rows, int T, float scale);
+/* SoftmaxBackward (:114) with scale 1; ScaledSoftmaxBackward (:125) with the scale. */
+int fh_op_softmax_backward(fh_context* ctx, const void* dout, const void* softmax_out, void* dx, int rows, int cols,
+                           float scale);
+/* GeluForward / GeluBackward (:134-135) over n floats. */
+int fh_op_gelu_forward(fh_context* ctx, const void* x, void* out, int64_t n);
+int fh_op_gelu_backward(fh_context* ctx, const void* dout, const void* x, void* dx, int64_t n);
+/* EmbeddingForward (:139): out[t,:] = table[indices[t],:]; EmbeddingBackward (:141):
+ * dtable[indices[t],:] += dout[t,:].  indices is a host array of n ids, each checked
+ * against the table's rows (FH_ERR_RANGE). */
+int fh_op_embedding_forward(fh_context* ctx, const void* table, int table_rows, const int32_t* indices, int n,
+                            void* out, int D);
+int fh_op_embedding_backward(fh_context* ctx, const void* dout, const int32_t* indices, int n, void* dtable,
+                             int table_rows, int D);
+/* CausalMask (:145) over len floats of packed [T,T] blocks. */
+int fh_op_causal_mask(fh_context* ctx, void* scores, int64_t len, int T);
+/* CrossEntropyForward (:154): probs (may alias logits) and the mean loss over the
+ * non-ignored targets (host array of T) in *loss; while a loss accumulation is active
+ * the loss stays on the device and *loss is 0.  BeginLossAccumulation /
+ * EndLossAccumulation (:159-161): the mean over every non-ignored target since begin;
+ * out-of-order calls return FH_ERR_STATE with the reference's messages.
+ * CrossEntropyBackward (:164): dlogits (may alias probs) = (probs - onehot) / count. */
+int fh_op_cross_entropy_forward(fh_context* ctx, const void* logits, const int32_t* targets, void* probs, int T,
+                                int V, int ignore_index, float* loss);
+int fh_op_begin_loss_accumulation(fh_context* ctx);
+int fh_op_end_loss_accumulation(fh_context* ctx, float* mean_loss);
+int fh_op_cross_entropy_backward(fh_context* ctx, const void* probs, const int32_t* targets, void* dlogits, int T,
+                                 int V, int ignore_index);
+/* SumSquares (:214) and GlobalSumSquares (:227): sum of x^2 in double, one readback. */
+int fh_op_sum_squares(fh_context* ctx, const void* x, int64_t n, double* out);
+int fh_op_global_sum_squares(fh_context* ctx, const void* const* xs, const int64_t* ns, int count, double* out);
+/* AdamWStep (:241): moments and weights of n elements; step is 1-based; weight decay
+ * applies when weight_decay != 0 and is_matrix (the tensor's rank is above 1). */
+int fh_op_adamw_step(fh_context* ctx, void* w, const void* g, void* m, void* v, int64_t n, float lr, float beta1,
+                     float beta2, float eps, float weight_decay, int step, int is_matrix);
+
 #ifdef __cplusplus
 }
 #endif

@@ -496,9 +496,256 @@ void apply_repetition_controls(float* l, int v, const int* hist, int n, float pe
 // ---------------------------------------------------------------------------
 // C ABI for the Python test harness (oracle/oracle.py).
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// The rest of the ITensorBackend contract on the CPU (CpuBackend.cs and the
+// interface defaults in ITensorBackend.cs), sequential: the checker for the
+// HIP op-level entry points.
+// ---------------------------------------------------------------------------
+
+// MatMulRowKernelSeq, CpuBackend.cs:118-131 with AddScaled :185-194: per row,
+// y (cleared unless accumulating) += a_k * b[k,:] for k ascending; a_k is
+// a[m,k] (NN) or a[k,m] (TN).
+void matmul_rows(const float* a, const float* b, float* y, int M, int K, int N, bool acc, bool a_t) {
+    for (int m = 0; m < M; m++) {
+        float* yr = y + (int64_t)m * N;
+        if (!acc)
+            for (int n = 0; n < N; n++) yr[n] = 0.f;
+        for (int k = 0; k < K; k++) {
+            const float s = a_t ? a[(int64_t)k * M + m] : a[(int64_t)m * K + k];
+            const float* br = b + (int64_t)k * N;
+            for (int n = 0; n < N; n++) yr[n] = yr[n] + s * br[n];
+        }
+    }
+}
+
+// MatMulNT's sequential branch, CpuBackend.cs:71-87: y (+)= Dot(a[m,:], b[n,:]).
+void matmul_nt_acc(const float* a, const float* b, float* y, int M, int K, int N, bool acc) {
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++) {
+            const float d = dot_net(a + (int64_t)m * K, b + (int64_t)n * K, K);
+            float& o = y[(int64_t)m * N + n];
+            o = acc ? o + d : d;
+        }
+}
+
+// Gelu derivative, CpuBackend.cs:490-499.
+inline float gelu_grad(float dout, float v) {
+    const float u = kGeluC * (v + 0.044715f * v * v * v);
+    const float t = std::tanh(u);
+    const float du = kGeluC * (1.f + 3.f * 0.044715f * v * v);
+    return dout * 0.5f * (1.f + t + v * (1.f - t * t) * du);
+}
+
 extern "C" {
 
 void or_set_threads(int n) { g_threads = n < 1 ? 1 : n; }
+
+// MatMulNN / NT / TN (CpuBackend.cs:37-115) and the Batched variants
+// (:198-221): mode 0 NN, 1 NT, 2 TN; slot s uses a + s*M*K, b + s*K*N, y + s*M*N.
+void or_op_matmul(int mode, const float* a, const float* b, float* y, int slots, int M, int K, int N, int acc) {
+    for (int s = 0; s < slots; s++) {
+        const float* as = a + (int64_t)s * M * K;
+        const float* bs = b + (int64_t)s * K * N;
+        float* ys = y + (int64_t)s * M * N;
+        if (mode == 1)
+            matmul_nt_acc(as, bs, ys, M, K, N, acc != 0);
+        else
+            matmul_rows(as, bs, ys, M, K, N, acc != 0, mode == 2);
+    }
+}
+
+// PackHeads / UnpackHeads, CpuBackend.cs:225-262.
+void or_op_pack_heads(const float* src, int src_cols, float* dst, int batch, int T, int H, int hd, int col_base) {
+    for (int q = 0; q < batch; q++)
+        for (int h = 0; h < H; h++)
+            for (int t = 0; t < T; t++)
+                std::memcpy(dst + ((int64_t)(q * H + h) * T + t) * hd, src + (int64_t)(q * T + t) * src_cols + col_base + h * hd,
+                            sizeof(float) * hd);
+}
+void or_op_unpack_heads(const float* src, float* dst, int dst_cols, int batch, int T, int H, int hd, int col_base) {
+    for (int q = 0; q < batch; q++)
+        for (int h = 0; h < H; h++)
+            for (int t = 0; t < T; t++)
+                std::memcpy(dst + (int64_t)(q * T + t) * dst_cols + col_base + h * hd, src + ((int64_t)(q * H + h) * T + t) * hd,
+                            sizeof(float) * hd);
+}
+
+void or_op_add_bias(float* y, const float* bias, int rows, int cols) { add_bias(y, bias, rows, cols); }
+
+// SumRows, CpuBackend.cs:293-300: dBias[c] += row[c], rows ascending.
+void or_op_sum_rows(const float* dy, float* dbias, int rows, int cols) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++) dbias[c] = dbias[c] + dy[(int64_t)r * cols + c];
+}
+
+void or_op_add_in_place(float* dst, const float* src, int64_t n) { add_in_place(dst, src, n); }
+
+// CopyBlock, CpuBackend.cs:325-331.
+void or_op_copy_block(const float* src, int src_cols, float* dst, int dst_cols, int src_row, int src_col, int dst_row,
+                      int dst_col, int rows, int cols) {
+    for (int r = 0; r < rows; r++)
+        std::memcpy(dst + (int64_t)(dst_row + r) * dst_cols + dst_col, src + (int64_t)(src_row + r) * src_cols + src_col,
+                    sizeof(float) * cols);
+}
+
+// Scale, CpuBackend.cs:334-346.
+void or_op_scale(float* x, int64_t n, float f) {
+    for (int64_t i = 0; i < n; i++) x[i] = x[i] * f;
+}
+
+// Transpose, CpuBackend.cs:349-357.
+void or_op_transpose(const float* x, float* out, int rows, int cols) {
+    for (int r = 0; r < rows; r++)
+        for (int c = 0; c < cols; c++) out[(int64_t)c * rows + r] = x[(int64_t)r * cols + c];
+}
+
+// LayerNormForward with the cached statistics, CpuBackend.cs:377-398.
+void or_op_layernorm_forward(const float* x, const float* w, const float* b, float* out, float* mean, float* rstd,
+                             int rows, int cols, float eps) {
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (int64_t)r * cols;
+        float sum = 0.f;
+        for (int c = 0; c < cols; c++) sum = sum + xr[c];
+        const float mu = sum / (float)cols;
+        float var_sum = 0.f;
+        for (int c = 0; c < cols; c++) {
+            const float dd = xr[c] - mu;
+            var_sum = var_sum + dd * dd;
+        }
+        const float rs = 1.f / std::sqrt(var_sum / (float)cols + eps);
+        mean[r] = mu;
+        rstd[r] = rs;
+        for (int c = 0; c < cols; c++) out[(int64_t)r * cols + c] = (xr[c] - mu) * rs * w[c] + b[c];
+    }
+}
+
+// LayerNormBackward, CpuBackend.cs:400-430: dW, dB accumulate; dX overwritten.
+void or_op_layernorm_backward(const float* dout, const float* x, const float* w, const float* mean, const float* rstd,
+                              float* dx, float* dw, float* db, int rows, int cols) {
+    const float inv_n = 1.f / (float)cols;
+    for (int r = 0; r < rows; r++) {
+        const float* dr = dout + (int64_t)r * cols;
+        const float* xr = x + (int64_t)r * cols;
+        float* dxr = dx + (int64_t)r * cols;
+        const float mu = mean[r], rs = rstd[r];
+        float s1 = 0.f, s2 = 0.f;
+        for (int c = 0; c < cols; c++) {
+            const float xhat = (xr[c] - mu) * rs;
+            const float dxhat = dr[c] * w[c];
+            dw[c] = dw[c] + dr[c] * xhat;
+            db[c] = db[c] + dr[c];
+            dxr[c] = dxhat;
+            s1 = s1 + dxhat;
+            s2 = s2 + dxhat * xhat;
+        }
+        const float m1 = s1 * inv_n, m2 = s2 * inv_n;
+        for (int c = 0; c < cols; c++) {
+            const float xhat = (xr[c] - mu) * rs;
+            dxr[c] = rs * (dxr[c] - m1 - xhat * m2);
+        }
+    }
+}
+
+// SoftmaxBackward, CpuBackend.cs:461-473.
+void or_op_softmax_backward(const float* dout, const float* s, float* dx, int rows, int cols) {
+    for (int r = 0; r < rows; r++) {
+        const float* dr = dout + (int64_t)r * cols;
+        const float* sr = s + (int64_t)r * cols;
+        float dot = 0.f;
+        for (int c = 0; c < cols; c++) dot = dot + dr[c] * sr[c];
+        for (int c = 0; c < cols; c++) dx[(int64_t)r * cols + c] = sr[c] * (dr[c] - dot);
+    }
+}
+
+void or_op_gelu_backward(const float* dout, const float* x, float* dx, int64_t n) {
+    for (int64_t i = 0; i < n; i++) dx[i] = gelu_grad(dout[i], x[i]);
+}
+
+// EmbeddingForward / EmbeddingBackward, CpuBackend.cs:530-543.
+void or_op_embedding_forward(const float* table, const int* idx, int n, float* out, int D) {
+    for (int t = 0; t < n; t++) std::memcpy(out + (int64_t)t * D, table + (int64_t)idx[t] * D, sizeof(float) * D);
+}
+void or_op_embedding_backward(const float* dout, const int* idx, int n, float* dtable, int D) {
+    for (int t = 0; t < n; t++) add_in_place(dtable + (int64_t)idx[t] * D, dout + (int64_t)t * D, D);
+}
+
+// CausalMask, CpuBackend.cs:551-557 over every packed [T,T] block of `len` floats.
+void or_op_causal_mask(float* scores, int64_t len, int T) {
+    for (int64_t o = 0; o < len; o += (int64_t)T * T)
+        for (int i = 0; i < T; i++)
+            for (int j = i + 1; j < T; j++) scores[o + (int64_t)i * T + j] = -INFINITY;
+}
+
+// CrossEntropyForward, CpuBackend.cs:594-622 (probs may alias logits).
+float or_op_cross_entropy_forward(const float* logits, const int* targets, float* probs, int T, int V, int ignore) {
+    float total = 0.f;
+    int count = 0;
+    for (int t = 0; t < T; t++) {
+        const float* lr = logits + (int64_t)t * V;
+        float* pr = probs + (int64_t)t * V;
+        const bool ignored = targets[t] == ignore;
+        const float tl = ignored ? 0.f : lr[targets[t]];
+        float mx = lr[0];
+        for (int v = 1; v < V; v++) mx = std::fmax(mx, lr[v]);
+        float sum = 0.f;
+        for (int v = 0; v < V; v++) {
+            pr[v] = std::exp(lr[v] - mx);
+            sum = sum + pr[v];
+        }
+        const float inv = 1.f / sum;
+        for (int v = 0; v < V; v++) pr[v] = pr[v] * inv;
+        if (!ignored) {
+            total = total + (std::log(sum) + mx - tl);
+            count++;
+        }
+    }
+    return count > 0 ? total / (float)count : 0.f;
+}
+
+// CrossEntropyBackward, CpuBackend.cs:625-644 (dLogits may alias probs).
+void or_op_cross_entropy_backward(const float* probs, const int* targets, float* dl, int T, int V, int ignore) {
+    int count = 0;
+    for (int t = 0; t < T; t++) count += targets[t] != ignore;
+    if (count == 0) {
+        std::memset(dl, 0, sizeof(float) * (size_t)T * V);
+        return;
+    }
+    const float scale = 1.f / (float)count;
+    for (int t = 0; t < T; t++) {
+        float* dr = dl + (int64_t)t * V;
+        const float* pr = probs + (int64_t)t * V;
+        if (targets[t] == ignore) {
+            std::memset(dr, 0, sizeof(float) * V);
+            continue;
+        }
+        for (int v = 0; v < V; v++) dr[v] = pr[v] * scale;
+        dr[targets[t]] = dr[targets[t]] - scale;
+    }
+}
+
+// ITensorBackend.SumSquares default, ITensorBackend.cs:214-220 (double sum).
+double or_op_sum_squares(const float* x, int64_t n) {
+    double s = 0;
+    for (int64_t i = 0; i < n; i++) s += (double)x[i] * x[i];
+    return s;
+}
+
+// ITensorBackend.AdamWStep default, ITensorBackend.cs:241-265; `matrix` is w.Rank > 1.
+void or_op_adamw(float* w, const float* g, float* m, float* v, int64_t n, float lr, float b1, float b2, float eps,
+                 float wd, int step, int matrix) {
+    const float bc1 = 1.f - std::pow(b1, (float)step);
+    const float bc2 = 1.f - std::pow(b2, (float)step);
+    const bool decay = wd != 0.f && matrix;
+    for (int64_t i = 0; i < n; i++) {
+        const float gi = g[i];
+        m[i] = b1 * m[i] + (1.f - b1) * gi;
+        v[i] = b2 * v[i] + (1.f - b2) * gi * gi;
+        if (decay) w[i] = w[i] - lr * wd * w[i];
+        const float mh = m[i] / bc1;
+        const float vh = v[i] / bc2;
+        w[i] = w[i] - lr * mh / (std::sqrt(vh) + eps);
+    }
+}
 
 void or_net_random_doubles(int seed, int n, double* out) {
     NetRandom r(seed);

@@ -61,6 +61,29 @@ def lib():
                                                   ctypes.c_void_p, _c_int, _c_float, _c_int, _c_int,
                                                   _i32p, ctypes.c_void_p])
         L.or_generate.restype = _c_int
+        i64, vp = ctypes.c_int64, ctypes.c_void_p
+        L.or_op_matmul.argtypes = [_c_int, _f32p, _f32p, _f32p] + [_c_int] * 5
+        L.or_op_pack_heads.argtypes = [_f32p, _c_int, _f32p] + [_c_int] * 5
+        L.or_op_unpack_heads.argtypes = [_f32p, _f32p] + [_c_int] * 6
+        L.or_op_add_bias.argtypes = [_f32p, _f32p, _c_int, _c_int]
+        L.or_op_sum_rows.argtypes = [_f32p, _f32p, _c_int, _c_int]
+        L.or_op_add_in_place.argtypes = [_f32p, _f32p, i64]
+        L.or_op_copy_block.argtypes = [_f32p, _c_int, _f32p] + [_c_int] * 7
+        L.or_op_scale.argtypes = [_f32p, i64, _c_float]
+        L.or_op_transpose.argtypes = [_f32p, _f32p, _c_int, _c_int]
+        L.or_op_layernorm_forward.argtypes = [_f32p] * 6 + [_c_int, _c_int, _c_float]
+        L.or_op_layernorm_backward.argtypes = [_f32p] * 8 + [_c_int, _c_int]
+        L.or_op_softmax_backward.argtypes = [_f32p, _f32p, _f32p, _c_int, _c_int]
+        L.or_op_gelu_backward.argtypes = [_f32p, _f32p, _f32p, i64]
+        L.or_op_embedding_forward.argtypes = [_f32p, _i32p, _c_int, _f32p, _c_int]
+        L.or_op_embedding_backward.argtypes = [_f32p, _i32p, _c_int, _f32p, _c_int]
+        L.or_op_causal_mask.argtypes = [_f32p, i64, _c_int]
+        L.or_op_cross_entropy_forward.argtypes = [vp, _i32p, vp, _c_int, _c_int, _c_int]
+        L.or_op_cross_entropy_forward.restype = _c_float
+        L.or_op_cross_entropy_backward.argtypes = [vp, _i32p, vp, _c_int, _c_int, _c_int]
+        L.or_op_sum_squares.argtypes = [_f32p, i64]
+        L.or_op_sum_squares.restype = _c_double
+        L.or_op_adamw.argtypes = [_f32p, _f32p, _f32p, _f32p, i64] + [_c_float] * 5 + [_c_int, _c_int]
         _lib = L
     return _lib
 
@@ -189,3 +212,119 @@ def generate(cfg: Config, weights: np.ndarray, prompt, max_new: int, temperature
     if return_logits:
         return ids, lg[:n].copy()
     return ids
+
+
+# ---- the rest of CpuBackend (training ops), in place on float32 arrays ------------------
+# Each wraps the or_op_* restatement in forge_oracle.cpp; arrays are modified in place
+# where the reference method writes, as the C# methods do on Tensor.Data.
+
+def _f(x):
+    assert isinstance(x, np.ndarray) and x.dtype == np.float32 and x.flags.c_contiguous
+    return x
+
+
+def op_matmul(mode: str, a, b, y, M, K, N, accumulate=False, slots=1):
+    """MatMulNN/NT/TN and the Batched variants (CpuBackend.cs:37-221), into y."""
+    lib().or_op_matmul({"nn": 0, "nt": 1, "tn": 2}[mode], _f(a), _f(b), _f(y), slots, M, K, N, int(accumulate))
+
+
+def op_pack_heads(src, src_cols, dst, batch, T, H, hd, col_base):
+    lib().or_op_pack_heads(_f(src), src_cols, _f(dst), batch, T, H, hd, col_base)
+
+
+def op_unpack_heads(src, dst, dst_cols, batch, T, H, hd, col_base):
+    lib().or_op_unpack_heads(_f(src), _f(dst), dst_cols, batch, T, H, hd, col_base)
+
+
+def op_add_bias(y, bias, rows, cols):
+    lib().or_op_add_bias(_f(y), _f(bias), rows, cols)
+
+
+def op_sum_rows(dy, dbias, rows, cols):
+    lib().or_op_sum_rows(_f(dy), _f(dbias), rows, cols)
+
+
+def op_add_in_place(dst, src):
+    lib().or_op_add_in_place(_f(dst), _f(src), dst.size)
+
+
+def op_copy_block(src, src_cols, dst, dst_cols, src_row, src_col, dst_row, dst_col, rows, cols):
+    lib().or_op_copy_block(_f(src), src_cols, _f(dst), dst_cols, src_row, src_col, dst_row, dst_col, rows, cols)
+
+
+def op_scale(x, factor):
+    lib().or_op_scale(_f(x), x.size, factor)
+
+
+def op_transpose(x, out, rows, cols):
+    lib().or_op_transpose(_f(x), _f(out), rows, cols)
+
+
+def op_layernorm_forward(x, w, b, out, mean, rstd, rows, cols, eps):
+    lib().or_op_layernorm_forward(_f(x), _f(w), _f(b), _f(out), _f(mean), _f(rstd), rows, cols, eps)
+
+
+def op_layernorm_backward(dout, x, w, mean, rstd, dx, dw, db, rows, cols):
+    lib().or_op_layernorm_backward(_f(dout), _f(x), _f(w), _f(mean), _f(rstd), _f(dx), _f(dw), _f(db), rows, cols)
+
+
+def op_softmax_forward(x, rows, cols):
+    lib().or_softmax(_f(x), rows, cols)
+
+
+def op_softmax_backward(dout, s, dx, rows, cols):
+    lib().or_op_softmax_backward(_f(dout), _f(s), _f(dx), rows, cols)
+
+
+def op_scaled_causal_softmax_forward(scores, rows, T, scale):
+    """ITensorBackend.cs:117-122: Scale, CausalMask, SoftmaxForward."""
+    op_scale(scores, scale)
+    op_causal_mask(scores, T)
+    op_softmax_forward(scores, rows, T)
+
+
+def op_scaled_softmax_backward(dout, s, dx, rows, cols, scale):
+    """ITensorBackend.cs:125-130: SoftmaxBackward, then Scale."""
+    op_softmax_backward(dout, s, dx, rows, cols)
+    op_scale(dx, scale)
+
+
+def op_gelu_forward(x, out):
+    lib().or_gelu(_f(x), _f(out), x.size)
+
+
+def op_gelu_backward(dout, x, dx):
+    lib().or_op_gelu_backward(_f(dout), _f(x), _f(dx), x.size)
+
+
+def op_embedding_forward(table, indices, out, D):
+    idx = np.ascontiguousarray(indices, np.int32)
+    lib().or_op_embedding_forward(_f(table), idx, idx.size, _f(out), D)
+
+
+def op_embedding_backward(dout, indices, dtable, D):
+    idx = np.ascontiguousarray(indices, np.int32)
+    lib().or_op_embedding_backward(_f(dout), idx, idx.size, _f(dtable), D)
+
+
+def op_causal_mask(scores, T):
+    lib().or_op_causal_mask(_f(scores), scores.size, T)
+
+
+def op_cross_entropy_forward(logits, targets, probs, T, V, ignore) -> float:
+    """probs may be logits itself (the in-place form)."""
+    tg = np.ascontiguousarray(targets, np.int32)
+    return float(lib().or_op_cross_entropy_forward(_f(logits).ctypes.data, tg, _f(probs).ctypes.data, T, V, ignore))
+
+
+def op_cross_entropy_backward(probs, targets, dlogits, T, V, ignore):
+    tg = np.ascontiguousarray(targets, np.int32)
+    lib().or_op_cross_entropy_backward(_f(probs).ctypes.data, tg, _f(dlogits).ctypes.data, T, V, ignore)
+
+
+def op_sum_squares(x) -> float:
+    return float(lib().or_op_sum_squares(_f(x), x.size))
+
+
+def op_adamw(w, g, m, v, lr, beta1, beta2, eps, weight_decay, step, is_matrix):
+    lib().or_op_adamw(_f(w), _f(g), _f(m), _f(v), w.size, lr, beta1, beta2, eps, weight_decay, step, int(is_matrix))
