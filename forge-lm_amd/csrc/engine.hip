@@ -973,6 +973,24 @@ int fh_session_destroy(fh_session* s) {
   return FH_OK;
 }
 
+int fh_init_weights(const fh_model_desc* desc, int32_t seed, float* out, int64_t n) {
+  FH_TRY(validate_desc(desc));
+  if (!out) return set_err(FH_ERR_INVALID, "null output");
+  auto reg = make_registry(*desc);
+  std::vector<int64_t> offs, sizes;
+  std::vector<int> kinds;
+  int64_t tot = 0;
+  for (auto& sl : reg) {
+    offs.push_back(tot);
+    sizes.push_back(sl.numel);
+    kinds.push_back(sl.init_kind);
+    tot += sl.numel;
+  }
+  if (n != tot) return set_err(FH_ERR_INVALID, "the registry holds %lld floats, not %lld", (long long)tot, (long long)n);
+  init_registry_random(seed, desc->n_layers, offs, sizes, kinds, out);
+  return FH_OK;
+}
+
 int fh_session_init_random(fh_session* s, int32_t seed) {
   if (!s) return set_err(FH_ERR_INVALID, "session is null");
   std::vector<int64_t> offs, sizes;

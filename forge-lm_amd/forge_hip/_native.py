@@ -30,7 +30,7 @@ EXPORTS = (
     "fh_context_info", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
     "fh_buffer_copy", "fh_matmul_nn",
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
-    "fh_session_init_random", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
+    "fh_session_init_random", "fh_init_weights", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_sample_logits",
     "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256", "fh_generate_begin", "fh_generate_next",
     # op-level ITensorBackend
@@ -109,6 +109,7 @@ def lib():
     L.fh_param_count.restype = i64
     L.fh_param_info.argtypes = [P(ModelDesc), ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t, P(i64)]
     L.fh_session_init_random.argtypes = [vp, i32]
+    L.fh_init_weights.argtypes = [P(ModelDesc), i32, vp, i64]
     L.fh_session_load_weights.argtypes = [vp, P(vp), ctypes.c_int]
     L.fh_session_read_param.argtypes = [vp, ctypes.c_int, vp, i64]
     L.fh_forward_last.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp]

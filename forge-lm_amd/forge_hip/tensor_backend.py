@@ -15,6 +15,7 @@ kernels on the stale device copy, as the contract states.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Optional, Sequence
 
 import numpy as np
@@ -72,13 +73,23 @@ class _Entry:
     """A tensor's device copy: host_stale = a kernel wrote it since the last download;
     device_stale = the host copy is authoritative (never uploaded, or invalidated)."""
 
-    __slots__ = ("buf", "host_stale", "device_stale", "backend")
+    __slots__ = ("buf", "host_stale", "device_stale", "backend", "__weakref__")
 
     def __init__(self, backend, buf):
         self.backend = backend
         self.buf = buf
         self.host_stale = False
         self.device_stale = True
+
+
+def _bucket(nbytes: int) -> int:
+    """Allocation size class: 256-byte granules up to 64 KiB, then steps of an
+    eighth of the power of two (waste below 12.5%)."""
+    n = max(256, int(nbytes))
+    if n <= 65536:
+        return (n + 255) // 256 * 256
+    step = 1 << (n.bit_length() - 4)
+    return (n + step - 1) // step * step
 
 
 class HipTensorBackend:
@@ -88,15 +99,30 @@ class HipTensorBackend:
         self._owns = backend is None
         self.backend = backend if backend is not None else HipBackend(device)
         self._ctx = self.backend.handle
-        self._entries = []
+        # device storage of collected tensors goes back to per-size free lists and
+        # is reused (the reference's device backends do the same, CudaBackend.cs:496-515);
+        # every use of a buffer is ordered on the context's stream, so reuse is safe
+        self._free = {}
+        self._all = []
 
     # ---- residency -----------------------------------------------------------------
+    def _release(self, size: int, buf: DeviceBuffer) -> None:
+        if self._free is not None:
+            self._free.setdefault(size, []).append(buf)
+
     def _entry(self, t: Tensor) -> _Entry:
         e = t.DeviceResource
         if e is None or e.backend is not self:
-            e = _Entry(self, DeviceBuffer(self.backend, max(4, t.Data.nbytes)))
+            size = _bucket(t.Data.nbytes)
+            pool = self._free.get(size)
+            if pool:
+                buf = pool.pop()
+            else:
+                buf = DeviceBuffer(self.backend, size)
+                self._all.append(buf)
+            e = _Entry(self, buf)
             t.DeviceResource = e
-            self._entries.append(e)
+            weakref.finalize(e, self._release, size, buf)
         return e
 
     def _read(self, t: Tensor):
@@ -326,9 +352,10 @@ class HipTensorBackend:
         pass
 
     def Dispose(self) -> None:
-        for e in self._entries:
-            e.buf.free()
-        self._entries = []
+        self._free = None
+        for buf in self._all:
+            buf.free()
+        self._all = []
         if self._owns and self.backend is not None:
             self.backend.dispose()
         self.backend = None

@@ -124,6 +124,9 @@ int64_t fh_param_count(const fh_model_desc* desc);
 /* Number of registry tensors, and the name/size of tensor i (registry order). */
 int fh_param_info(const fh_model_desc* desc, int index, char* name, size_t name_len, int64_t* numel);
 int fh_session_init_random(fh_session* s, int32_t seed);
+/* The same initial weights into a host array of n floats (registry order): the GptModel
+ * constructor's init from new Random(seed) (GptModel.cs:38-99), without a device. */
+int fh_init_weights(const fh_model_desc* desc, int32_t seed, float* out, int64_t n);
 /* tensors[i] points at registry tensor i (fp32, host); n must equal the registry size. */
 int fh_session_load_weights(fh_session* s, const float* const* tensors, int n);
 /* Copies the device copy of registry tensor `index` back as fp32 (bf16 sessions widen). */
