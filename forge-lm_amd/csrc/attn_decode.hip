@@ -18,6 +18,7 @@ namespace {
 
 constexpr int KW = 64;        // keys per wave
 constexpr int CHUNK = 4 * KW;  // keys per block
+static_assert(CHUNK == kAttnDecodeChunk, "chunk size shared with the GEMM's attention operand");
 
 __device__ __forceinline__ float row16_sum(float v) {
   v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
 
 template <typename KT>
 hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
-                                   const KT* kcache, const KT* vcache, float* part, float* o) {
+                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine) {
   if (B <= 0 || H <= 0 || d != 64 * H || ctx <= 0 || (size_t)ctx * 64 * sizeof(KT) > 0x7fffffffu || !qkv ||
       !kcache || !vcache || !part || !o)
     return hipErrorInvalidValue;
@@ -148,13 +149,13 @@ hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv,
   hipLaunchKernelGGL(k_attn_decode_wide<KT>, dim3(maxc, H, B), dim3(256), 0, st, src, qkv, d, H, ctx, kcache, vcache,
                      part, maxc);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !combine) return e;
   return launch_attn_decode_combine(st, src, B, d, H, ctx, part, CHUNK, maxc, o);
 }
 
 template hipError_t launch_attn_decode_wide<float>(hipStream_t, RowSrc, const float*, int, int, int, int,
-                                                   const float*, const float*, float*, float*);
+                                                   const float*, const float*, float*, float*, bool);
 template hipError_t launch_attn_decode_wide<bf16_t>(hipStream_t, RowSrc, const float*, int, int, int, int,
-                                                    const bf16_t*, const bf16_t*, float*, float*);
+                                                    const bf16_t*, const bf16_t*, float*, float*, bool);
 
 }  // namespace fh

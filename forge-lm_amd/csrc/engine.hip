@@ -442,6 +442,42 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     // mproj reduction applies LN_f, so xn holds the head's input on return
     const int L = s->d.n_layers;
     LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
+    if (B > 4 && D == 64 * H && C <= 4 * kAttnDecodeChunk) {
+      // the attention combine is folded into the attn.proj GEMM's operand load
+      // (9 launches per layer); folding the mlp.fc reduction into mlp.proj's
+      // operand load was measured slower (each mlp.proj block re-reads 8 partials
+      // of its A chunk: 19 MB per layer)
+      const int cus = s->ctx->props.multiProcessorCount;
+      for (int l = 0; l < L; l++) {
+        WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+        WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+        int S = 0;
+        LAUNCH(launch_gemm_mfma_split<WT>(st, s->xn, B, D, s->wt<WT>(s->idx_blk(l, 2)), 3 * D, s->part,
+                                          s->part_floats, cus, &S));
+        LAUNCH(launch_epilogue_qkv<WT>(st, s->part, S, B, D, s->v(s->idx_blk(l, 3)), s->qkv, src, 1, H, C, kc, vc));
+        LAUNCH(launch_attn_decode_wide<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, s->o, false));
+        AOperand ao{};
+        ao.kind = AOP_ATTN;
+        ao.apart = s->apart;
+        ao.src = src;
+        ao.H = H;
+        ao.ctx = C;
+        ao.chunk = kAttnDecodeChunk;
+        ao.maxc = (C + kAttnDecodeChunk - 1) / kAttnDecodeChunk;
+        LAUNCH(launch_gemm_mfma_split<WT>(st, s->apart, B, D, s->wt<WT>(s->idx_blk(l, 4)), D, s->part,
+                                          s->part_floats, cus, &S, &ao));
+        LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 5)), s->x, s->x2, s->v(s->idx_blk(l, 6)),
+                                  s->v(s->idx_blk(l, 7)), s->xn, 1e-5f));
+        FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+                          s->h));
+        LAUNCH(launch_gemm_mfma_split<WT>(st, s->h, B, 4 * D, s->wt<WT>(s->idx_blk(l, 10)), D, s->part,
+                                          s->part_floats, cus, &S));
+        const size_t ln = l + 1 < L ? s->idx_blk(l + 1, 0) : s->idx_lnf();
+        LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 11)), s->x2, s->x, s->v(ln),
+                                  s->v(ln + 1), s->xn, 1e-5f));
+      }
+      return FH_OK;
+    }
     for (int l = 0; l < L; l++) {
       WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
       WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;

@@ -49,16 +49,59 @@ struct Tr<float> {
   typedef float elem;
 };
 
+// Four consecutive A values A[m][k..k+3] built from decode attention's chunk
+// partials (AOperand): rows past M repeat the last row (their products are
+// dropped).  The chunk loop runs to a fixed count on clamped addresses, so every
+// load of a stage issues at once; chunks past the real count are skipped.
+constexpr int kAttnChunksMax = 4;
+__device__ __forceinline__ float4 load_attn_a4(const AOperand& ao, int m, int k, int M, int K) {
+  // k_attn_decode_combine for sequence r, head k / hd, dims e .. e+3
+  const int r = min(m, M - 1);
+  {
+    const int hd = K / ao.H, h = k / hd, e = k % hd;
+    const int n = *ao.src.step;
+    const int nkeys = min(ao.ctx, ao.src.pos_off + ao.src.pos_mul * n + 1);
+    const int nch = (nkeys + ao.chunk - 1) / ao.chunk;
+    const float* P0 = ao.apart + ((size_t)r * ao.H + h) * ao.maxc * (hd + 2);
+    float mc[kAttnChunksMax], lc[kAttnChunksMax], pc[kAttnChunksMax][4];
+#pragma unroll
+    for (int c = 0; c < kAttnChunksMax; c++) {
+      const float* P = P0 + (size_t)min(c, nch - 1) * (hd + 2);
+      mc[c] = P[hd];
+      lc[c] = P[hd + 1];
+#pragma unroll
+      for (int j = 0; j < 4; j++) pc[c][j] = P[e + j];
+    }
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kAttnChunksMax; c++)
+      if (c < nch) Mx = fmaxf(Mx, mc[c]);
+    float L = 0.f, a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int c = 0; c < kAttnChunksMax; c++)
+      if (c < nch) {
+        const float f = expf(mc[c] - Mx);
+        L += lc[c] * f;
+        a0 += pc[c][0] * f;
+        a1 += pc[c][1] * f;
+        a2 += pc[c][2] * f;
+        a3 += pc[c][3] * f;
+      }
+    const float inv = 1.f / L;
+    return make_float4(a0 * inv, a1 * inv, a2 * inv, a3 * inv);
+  }
+}
+
 // NSR == 0: K streams through a double-buffered LDS pair, one stage ahead.
 // NSR > 0 (short K chunks of split-K decode GEMMs, at most NSR stages): every
 // stage's loads are issued at once into NSR register sets and LDS buffers, so
 // the block pays one memory latency instead of one per stage.
-template <typename WT, int BM, int EPI, bool RES, int NSR>
+template <typename WT, int BM, int EPI, bool RES, int NSR, int AOP = AOP_PLAIN>
 __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, int M, int K,
                                                   const WT* __restrict__ Wt, int N, int kchunk,
                                                   const float* __restrict__ bias,
                                                   const float* __restrict__ res, float* __restrict__ Y,
-                                                  float* __restrict__ part) {
+                                                  float* __restrict__ part, AOperand ao) {
   using E = typename Tr<WT>::elem;
   constexpr int LDK = Tr<WT>::LDK;
   constexpr int MT = BM / 32;  // MFMA tiles along M per wave
@@ -89,8 +132,12 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
 #pragma unroll
     for (int i = 0; i < AV; i++) {
       const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsa, (row * K + k0 + 4 * kq) * 4, 0, 0);
-      a[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      if constexpr (AOP != AOP_PLAIN) {
+        a[i] = load_attn_a4(ao, m0 + row, k0 + 4 * kq, M, K);
+      } else {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rsa, (row * K + k0 + 4 * kq) * 4, 0, 0);
+        a[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+      }
     }
     constexpr int PER_ROW = BK * (int)sizeof(WT) / 16;  // 16-byte pieces per W row and stage
 #pragma unroll
@@ -236,18 +283,19 @@ template <typename WT, int BM, int NSR>
 static hipError_t launch_epi(hipStream_t st, dim3 grid, const float* a, int M, int K, const WT* Wt, int N, int kchunk,
                              const float* bias, int epi, const float* res, float* y, float* part) {
   const bool gelu = epi == EPI_GELU;
+  const AOperand ao{};
   if (part || (!gelu && !res))
     hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, false, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
-                       bias, res, y, part);
+                       bias, res, y, part, ao);
   else if (!gelu)
     hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, true, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
-                       bias, res, y, part);
+                       bias, res, y, part, ao);
   else if (!res)
     hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, false, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
-                       bias, res, y, part);
+                       bias, res, y, part, ao);
   else
     hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_GELU, true, NSR>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
-                       bias, res, y, part);
+                       bias, res, y, part, ao);
   return hipGetLastError();
 }
 
@@ -283,12 +331,37 @@ hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const 
   return launch_splitk_epilogue(st, part, S, M, N, bias, epi, res, y);
 }
 
+template <typename WT, int BM, int NSR, int AOP>
+static hipError_t launch_parts(hipStream_t st, dim3 grid, const float* a, int M, int K, const WT* Wt, int N,
+                               int kchunk, float* part, const AOperand& ao) {
+  hipLaunchKernelGGL((k_gemm_mfma<WT, BM, EPI_NONE, false, NSR, AOP>), grid, dim3(256), 0, st, a, M, K, Wt, N, kchunk,
+                     nullptr, nullptr, part, part, ao);
+  return hipGetLastError();
+}
+
+template <typename WT, int AOP>
+static hipError_t launch_parts_bm(hipStream_t st, dim3 grid, int bm, bool resident, const float* a, int M, int K,
+                                  const WT* Wt, int N, int kchunk, float* part, const AOperand& ao) {
+  if (bm == 128) return launch_parts<WT, 128, 0, AOP>(st, grid, a, M, K, Wt, N, kchunk, part, ao);
+  if (bm == 64)
+    return resident ? launch_parts<WT, 64, 3, AOP>(st, grid, a, M, K, Wt, N, kchunk, part, ao)
+                    : launch_parts<WT, 64, 0, AOP>(st, grid, a, M, K, Wt, N, kchunk, part, ao);
+  return resident ? launch_parts<WT, 32, 3, AOP>(st, grid, a, M, K, Wt, N, kchunk, part, ao)
+                  : launch_parts<WT, 32, 0, AOP>(st, grid, a, M, K, Wt, N, kchunk, part, ao);
+}
+
 template <typename WT>
 hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, float* part,
-                                  size_t part_floats, int cus, int* splits) {
-  if (!a || !Wt || !part || !splits || M <= 0 || N <= 0 || K <= 0 || K % BK != 0 || (size_t)M * N > part_floats)
+                                  size_t part_floats, int cus, int* splits, const AOperand* aop) {
+  if (!Wt || !part || !splits || M <= 0 || N <= 0 || K <= 0 || K % BK != 0 || (size_t)M * N > part_floats)
     return hipErrorInvalidValue;
   if ((size_t)128 * K * 4 > 0x7fffffffu) return hipErrorInvalidValue;
+  const int kind = aop ? aop->kind : AOP_PLAIN;
+  if (kind == AOP_PLAIN && !a) return hipErrorInvalidValue;
+  if (kind == AOP_ATTN && (!aop->apart || aop->H <= 0 || K % aop->H != 0 || (K / aop->H) % 4 != 0 ||
+                           aop->chunk <= 0 || aop->maxc <= 0 || aop->maxc > kAttnChunksMax || !aop->src.step ||
+                           (size_t)aop->maxc * aop->chunk < (size_t)aop->ctx))
+    return hipErrorInvalidValue;
   const int gn = (N + BN - 1) / BN;
   const int bm = M > 64 ? 128 : (M > 32 ? 64 : 32);
   const int gm = (M + bm - 1) / bm;
@@ -299,18 +372,16 @@ hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, 
   const int kchunk = K / S;
   dim3 grid(gn, gm, S);
   const bool resident = kchunk <= 3 * BK;
-  if (bm == 128) return launch_epi<WT, 128, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
-  if (bm == 64)
-    return resident ? launch_epi<WT, 64, 3>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part)
-                    : launch_epi<WT, 64, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
-  return resident ? launch_epi<WT, 32, 3>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part)
-                  : launch_epi<WT, 32, 0>(st, grid, a, M, K, Wt, N, kchunk, nullptr, EPI_NONE, nullptr, part, part);
+  const AOperand none{};
+  if (kind == AOP_ATTN)
+    return launch_parts_bm<WT, AOP_ATTN>(st, grid, bm, resident, a, M, K, Wt, N, kchunk, part, *aop);
+  return launch_parts_bm<WT, AOP_PLAIN>(st, grid, bm, resident, a, M, K, Wt, N, kchunk, part, none);
 }
 
 template hipError_t launch_gemm_mfma_split<float>(hipStream_t, const float*, int, int, const float*, int, float*,
-                                                  size_t, int, int*);
+                                                  size_t, int, int*, const AOperand*);
 template hipError_t launch_gemm_mfma_split<bf16_t>(hipStream_t, const float*, int, int, const bf16_t*, int, float*,
-                                                   size_t, int, int*);
+                                                   size_t, int, int*, const AOperand*);
 template hipError_t launch_transpose<float>(hipStream_t, const float*, int, int, float*);
 template hipError_t launch_transpose<bf16_t>(hipStream_t, const bf16_t*, int, int, bf16_t*);
 template hipError_t launch_gemm_mfma<float>(hipStream_t, const float*, int, int, const float*, int, const float*, int,

@@ -83,9 +83,11 @@ hipError_t launch_attn_decode_combine(hipStream_t st, RowSrc src, int B, int d, 
 
 // The same decode attention for head_dim 64 (attn_decode.hip): 256-key chunks,
 // one 1 KB request per 4 K or V rows.  part must hold B*H*ceil(ctx/256)*66 floats.
+// Without `combine` only the chunk partials are written (the consumer combines).
+constexpr int kAttnDecodeChunk = 256;
 template <typename KT>
 hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
-                                   const KT* kcache, const KT* vcache, float* part, float* o);
+                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine = true);
 
 // Tied head for B rows: logits[b, v] = dot(xn[b,:], E[v,:]).
 template <typename WT>
@@ -123,11 +125,24 @@ struct GemmBf16Out {
 hipError_t launch_gemm_bf16_qkv(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, const float* bias,
                                 RowSrc src, int T, int H, int ctx, bf16_t* q, bf16_t* kcache, bf16_t* vcache);
 
+// Where a split-K GEMM's A operand [M][K] comes from.  AOP_ATTN: decode
+// attention's chunk partials apart[(b*H + h)*maxc + c][hd + 2] of row b combined
+// as k_attn_decode_combine does (keys 0..pos, pos from src): the A values equal
+// what the combine kernel would have written, without that launch.
+enum AOpKind : int { AOP_PLAIN = 0, AOP_ATTN = 2 };
+struct AOperand {
+  int kind;
+  const float* apart;
+  RowSrc src;
+  int H, ctx, chunk, maxc;
+};
+
 // The same GEMM writing only the split-K partials part[S][M][N] (S >= 1, returned
-// in *splits) for a fused epilogue to reduce.
+// in *splits) for a fused epilogue to reduce; A is `a` or, with aop, built from
+// the producer's partials (AOP_ATTN: at most 4 chunks, ctx <= 1024).
 template <typename WT>
 hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, float* part,
-                                  size_t part_floats, int cus, int* splits);
+                                  size_t part_floats, int cus, int* splits, const AOperand* aop = nullptr);
 
 // Wt[n][k] = W[k][n].
 template <typename WT>
