@@ -116,3 +116,33 @@ def test_generate_validation_before_device_work(fhp):
         S.generate(Stub(), [1], 1, 1.0, 0, fhp.Random(1), eos_id=32)
     with pytest.raises(ValueError, match="Temperature"):
         S.generate(Stub(), [1], 1, float("nan"), 0, fhp.Random(1))
+
+
+def test_op_entry_points_reject_a_null_context(fhp):
+    # every fh_op_* validates its context before touching a device
+    import ctypes as C
+    L = fhp.lib()
+    buf = (C.c_float * 4)()
+    loss, dbl = C.c_float(), C.c_double()
+    calls = [
+        lambda: L.fh_op_matmul_nn(None, buf, buf, buf, 1, 1, 1, 1, 0),
+        lambda: L.fh_op_scale(None, buf, 4, 2.0),
+        lambda: L.fh_op_zero(None, buf, 4),
+        lambda: L.fh_op_layernorm_forward(None, buf, buf, buf, buf, buf, buf, 1, 4, 1e-5),
+        lambda: L.fh_op_cross_entropy_forward(None, buf, (C.c_int32 * 1)(0), buf, 1, 4, -1, C.byref(loss)),
+        lambda: L.fh_op_begin_loss_accumulation(None),
+        lambda: L.fh_op_sum_squares(None, buf, 4, C.byref(dbl)),
+        lambda: L.fh_op_adamw_step(None, buf, buf, buf, buf, 4, 1e-3, 0.9, 0.95, 1e-8, 0.1, 1, 1),
+    ]
+    for call in calls:
+        assert call() == fhp._native.FH_ERR_INVALID
+        assert "null context" in fhp._native.last_error()
+
+
+def test_init_weights_rejects_a_wrong_size(fhp):
+    import ctypes as C
+    cfg = fhp.ModelConfig(32, 8, 16, 2, 2)
+    desc = fhp.model._desc(cfg, 1, "f32")
+    w = np.empty(10, np.float32)
+    assert fhp.lib().fh_init_weights(C.byref(desc), 1, w.ctypes.data, 10) == fhp._native.FH_ERR_INVALID
+    assert "registry holds" in fhp._native.last_error()
