@@ -153,72 +153,46 @@ __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __rest
 }
 
 // Split-K reduction (k_splitk_epilogue's sum, bias, residual) fused with the
-// LayerNorm that follows: one block per row writes the row to y and its
-// LayerNorm to out, with k_layernorm's per-thread columns and reductions, so
-// both outputs equal the two separate kernels' bit for bit.  N <= 1024.
-__global__ __launch_bounds__(256) void k_epilogue_ln(const float* __restrict__ part, int S, int M, int N,
-                                                     const float* __restrict__ bias, const float* __restrict__ res,
-                                                     float* __restrict__ y, const float* __restrict__ w,
-                                                     const float* __restrict__ b, float* __restrict__ out,
-                                                     float eps) {
-  __shared__ float red[4];
-  const int r = blockIdx.x;
-  // partials through a bounded resource: 8 partials of the thread's 4 columns in
-  // flight together, skipped ones (past S or N) read as zeros; each column sums
-  // its partials in order, and the zeros after the last one change nothing
+// LayerNorm that follows: one 1024-thread block per row (a thread per column)
+// writes the row to y, exactly as k_splitk_epilogue would, and its LayerNorm to
+// out, with k_layernorm's formula over block sums.  N <= 1024.
+__global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ part, int S, int M, int N,
+                                                      const float* __restrict__ bias, const float* __restrict__ res,
+                                                      float* __restrict__ y, const float* __restrict__ w,
+                                                      const float* __restrict__ b, float* __restrict__ out,
+                                                      float eps) {
+  __shared__ float red[16];
+  const int r = blockIdx.x, c = threadIdx.x;
+  const bool on = c < N;
+  // one column per thread, up to 32 of its partials in flight together through a
+  // bounded resource (skipped ones, past S or N, read as zeros); the partials add
+  // in order, and the zeros after the last one change nothing
   const int pbytes = (int)((size_t)S * M * N * 4);
   const __amdgpu_buffer_rsrc_t rp =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part), (short)0, pbytes, 0x00020000);
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int i0 = 0; i0 < S; i0 += 8) {
-    float t[8][4];
+  float v = 0.f;
+  for (int i0 = 0; i0 < S; i0 += 32) {
+    float t[32];
 #pragma unroll
-    for (int ii = 0; ii < 8; ii++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int c = threadIdx.x + 256 * q;
-        const int off =
-            (c < N && i0 + ii < S) ? (int)((((size_t)(i0 + ii) * M + r) * N + c) * 4) : pbytes;
-        t[ii][q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
-      }
-#pragma unroll
-    for (int ii = 0; ii < 8; ii++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) v[q] += t[ii][q];
-  }
-  float s = 0.f;
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int c = threadIdx.x + 256 * q;
-    if (c < N) {
-      const size_t idx = (size_t)r * N + c;
-      float a = v[q];
-      if (bias) a += bias[c];
-      if (res) a += res[idx];
-      y[idx] = a;
-      v[q] = a;
-      s += a;
-    } else {
-      v[q] = 0.f;
+    for (int ii = 0; ii < 32; ii++) {
+      const int off = (on && i0 + ii < S) ? (int)((((size_t)(i0 + ii) * M + r) * N + c) * 4) : pbytes;
+      t[ii] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
     }
-  }
-  const float mu = block_sum<256>(s, red) / (float)N;
-  float var = 0.f;
 #pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int c = threadIdx.x + 256 * q;
-    if (c < N) {
-      const float dd = v[q] - mu;
-      var += dd * dd;
-    }
+    for (int ii = 0; ii < 32; ii++) v += t[ii];
   }
-  const float vs = block_sum<256>(var, red);
-  const float rs = 1.f / sqrtf(vs / (float)N + eps);
-#pragma unroll
-  for (int q = 0; q < 4; q++) {
-    const int c = threadIdx.x + 256 * q;
-    if (c < N) out[(size_t)r * N + c] = (v[q] - mu) * rs * w[c] + b[c];
+  const size_t idx = (size_t)r * N + c;
+  if (on) {
+    if (bias) v += bias[c];
+    if (res) v += res[idx];
+    y[idx] = v;
+  } else {
+    v = 0.f;
   }
+  const float mu = block_sum<1024>(v, red) / (float)N;
+  const float dd = on ? v - mu : 0.f;
+  const float rs = 1.f / sqrtf(block_sum<1024>(dd * dd, red) / (float)N + eps);
+  if (on) out[idx] = dd * rs * w[c] + b[c];
 }
 
 // Split-K reduction of a qkv projection (sum + bias into qkv) fused with the KV
@@ -1468,7 +1442,7 @@ hipError_t launch_epilogue_ln(hipStream_t st, const float* part, int splits, int
                               const float* res, float* y, const float* w, const float* b, float* out, float eps) {
   FH_CHECK_ARG(splits >= 1 && M > 0 && N > 0 && N <= 1024 && part && y && w && b && out &&
                (size_t)splits * M * N * 4 < 0x7fffffffu);
-  hipLaunchKernelGGL(k_epilogue_ln, dim3(M), dim3(256), 0, st, part, splits, M, N, bias, res, y, w, b, out, eps);
+  hipLaunchKernelGGL(k_epilogue_ln, dim3(M), dim3(1024), 0, st, part, splits, M, N, bias, res, y, w, b, out, eps);
   return hipGetLastError();
 }
 
