@@ -30,6 +30,15 @@
 //   dot lane order ....... parity unpinned: Vector<float>.Count=8 and the
 //                          Vector.Sum lane order are .NET JIT details.
 //   sampler .............. pinned by every InferenceTests literal.
+//   or_op_* (the rest of CpuBackend: training ops, ITensorBackend defaults)
+//                          pinned in tests/test_tensor_backend.py by the reference's
+//                          CpuBackendTests literals (matmuls vs float64 brute force,
+//                          cross-entropy hand literal, aliased = separate CE,
+//                          AddBias/SumRows/Scale/AddInPlace/Transpose, embedding,
+//                          causal mask), numpy restatements of the index-only ops
+//                          (head packing, CopyBlock), central-difference gradient
+//                          checks of every backward op against the forward, the
+//                          AdamW first-step closed form and the LayerNorm statistics.
 //   forward .............. KV-cached decode == full recompute bit-for-bit,
 //                          ForwardLast == last row of Forward exactly,
 //                          parameter counts 7232 / 97,934,592 / 219,237,376.

@@ -159,6 +159,21 @@ def test_oracle_heads_block_mask_embedding(oracle):
     np.testing.assert_array_equal(out.reshape(4, 3), table.reshape(5, 3)[[0, 2, 2, 4]])
 
 
+def test_oracle_layernorm_forward_statistics(oracle):
+    # LayerNormForward with its cached statistics: out equals the inference
+    # restatement bit for bit, mean and rstd are the row's mean and 1/sqrt(var+eps)
+    rng = NetRng(oracle, 104)
+    rows, cols, eps = 5, 48, 1e-5
+    x, w, b = rng.rand(rows * cols), rng.rand(cols), rng.rand(cols)
+    out, mean, rstd = np.zeros(rows * cols, np.float32), np.zeros(rows, np.float32), np.zeros(rows, np.float32)
+    oracle.op_layernorm_forward(x, w, b, out, mean, rstd, rows, cols, eps)
+    ref = oracle.layernorm(x.reshape(rows, cols), w, b, eps)
+    np.testing.assert_array_equal(out.reshape(rows, cols), ref)
+    X = x.reshape(rows, cols).astype(np.float64)
+    np.testing.assert_allclose(mean, X.mean(1), atol=1e-6)
+    np.testing.assert_allclose(rstd, 1 / np.sqrt(X.var(1) + eps), rtol=1e-5)
+
+
 def test_oracle_cross_entropy_hand_literal(oracle):
     # CpuBackendTests.CrossEntropy_MatchesLogSoftmax
     T, V = 3, 4
