@@ -412,6 +412,38 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
     if (s->bf16_act && M >= 256 && D % 64 == 0 && D == 64 * H)
       return enqueue_layers_window_bf16(s, T, src);
   }
+  if (M > 4 && D % 32 == 0 && D <= 1024 && (size_t)M * 3 * D <= s->part_floats) {
+    // short windows: the split-K reductions also store K/V and apply LN2 and the
+    // next layer's LN1, as in batched decode (the last mlp.proj keeps its residual
+    // epilogue: LN_f runs on the last rows only)
+    const int L = s->d.n_layers;
+    LAUNCH(launch_layernorm(st, s->x, M, M, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
+    for (int l = 0; l < L; l++) {
+      WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+      WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+      int S = 0;
+      FH_TRY(linear_parts<WT>(s, s->xn, M, D, s->idx_blk(l, 2), 3 * D, &S));
+      LAUNCH(launch_epilogue_qkv<WT>(st, s->part, S, M, D, s->v(s->idx_blk(l, 3)), s->qkv, src, T, H, C, kc, vc));
+      if (D == 64 * H)
+        LAUNCH((launch_attn_prefill_mfma<WT, float>(st, s->qkv, B, T, D, H, C, kc, vc, s->o)));
+      else
+        LAUNCH(launch_attn_prefill<WT>(st, s->qkv, B, T, D, H, C, kc, vc, s->o));
+      FH_TRY(linear_parts<WT>(s, s->o, M, D, s->idx_blk(l, 4), D, &S));
+      LAUNCH(launch_epilogue_ln(st, s->part, S, M, D, s->v(s->idx_blk(l, 5)), s->x, s->x2, s->v(s->idx_blk(l, 6)),
+                                s->v(s->idx_blk(l, 7)), s->xn, 1e-5f));
+      FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr,
+                        s->h));
+      if (l + 1 < L) {
+        FH_TRY(linear_parts<WT>(s, s->h, M, 4 * D, s->idx_blk(l, 10), D, &S));
+        LAUNCH(launch_epilogue_ln(st, s->part, S, M, D, s->v(s->idx_blk(l, 11)), s->x2, s->x,
+                                  s->v(s->idx_blk(l + 1, 0)), s->v(s->idx_blk(l + 1, 1)), s->xn, 1e-5f));
+      } else {
+        FH_TRY(linear<WT>(s, s->h, M, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, s->x2,
+                          s->x));
+      }
+    }
+    return FH_OK;
+  }
   for (int l = 0; l < s->d.n_layers; l++) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
