@@ -47,11 +47,10 @@ __device__ __forceinline__ float4 load4<bf16_t>(__amdgpu_buffer_rsrc_t r, int el
                      __uint_as_float(v.y & 0xffff0000u));
 }
 
-template <typename KT>
+template <typename KT, bool FROM_PARTS>
 __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const float* __restrict__ qkv, int d, int H,
-                                                          int ctx, const KT* __restrict__ kc,
-                                                          const KT* __restrict__ vc, float* __restrict__ part,
-                                                          int maxc) {
+                                                          int ctx, KT* __restrict__ kc, KT* __restrict__ vc,
+                                                          float* __restrict__ part, int maxc, QkvParts qp) {
   __shared__ float wm[4], wl[4];
   __shared__ __align__(16) float wo[4][64];
   const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -59,11 +58,49 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
   const int n = *src.step;
   const int nkeys = min(ctx, src.pos_off + src.pos_mul * n + 1);
   if (c * CHUNK >= nkeys) return;  // the whole block: no chunk of keys here
+  const size_t head = ((size_t)b * H + h) * ctx * 64;
+  float4 qr;
+  if constexpr (FROM_PARTS) {
+    // the qkv projection's split-K partials summed here (k_epilogue_qkv's order:
+    // 0 + partials + bias); the block whose chunk holds the new position first
+    // writes the new K and V rows into the caches, which its loads below then read
+    const size_t N3 = (size_t)3 * d, MN = (size_t)qp.M * N3;
+    const float* p0 = qp.part + (size_t)b * N3;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
+    for (int i = 0; i < qp.S; i++) {
+      const float4 v = *reinterpret_cast<const float4*>(p0 + i * MN + h * 64 + d4);
+      a.x += v.x;
+      a.y += v.y;
+      a.z += v.z;
+      a.w += v.w;
+    }
+    if (qp.bias) {
+      const float4 bb = *reinterpret_cast<const float4*>(qp.bias + h * 64 + d4);
+      a.x += bb.x;
+      a.y += bb.y;
+      a.z += bb.z;
+      a.w += bb.w;
+    }
+    qr = a;
+    const int pos = src.pos_off + src.pos_mul * n;
+    if ((unsigned)pos < (unsigned)ctx && c == pos / CHUNK) {
+      if (tid < 128) {
+        const int col = (tid < 64 ? d : 2 * d) + h * 64 + (tid & 63);
+        float v = 0.f;
+#pragma unroll 8
+        for (int i = 0; i < qp.S; i++) v += p0[i * MN + col];
+        if (qp.bias) v += qp.bias[col];
+        (tid < 64 ? kc : vc)[head + (size_t)pos * 64 + (tid & 63)] = from_f32<KT>(v);
+      }
+      __syncthreads();  // the new rows are stored before any wave reads them
+    }
+  } else {
+    qr = *reinterpret_cast<const float4*>(qkv + (size_t)b * 3 * d + h * 64 + d4);
+  }
   // q scaled by 1/sqrt(64) = 2^-3: exact, so q'.k = (q.k) / 8 bit for bit
-  const float4 qr = *reinterpret_cast<const float4*>(qkv + (size_t)b * 3 * d + h * 64 + d4);
   const float4 q4 = make_float4(qr.x * 0.125f, qr.y * 0.125f, qr.z * 0.125f, qr.w * 0.125f);
   const int j0 = c * CHUNK + w * KW;  // this wave's first key
-  const size_t head = ((size_t)b * H + h) * ctx * 64;
   // a wave past the last key fetches nothing (an empty buffer resource reads zeros)
   const int bytes = j0 < nkeys ? ctx * 64 * (int)sizeof(KT) : 0;
   const __amdgpu_buffer_rsrc_t rk =
@@ -141,21 +178,30 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
 
 template <typename KT>
 hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
-                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine) {
-  if (B <= 0 || H <= 0 || d != 64 * H || ctx <= 0 || (size_t)ctx * 64 * sizeof(KT) > 0x7fffffffu || !qkv ||
-      !kcache || !vcache || !part || !o)
+                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine,
+                                   const QkvParts* qp) {
+  if (B <= 0 || H <= 0 || d != 64 * H || ctx <= 0 || (size_t)ctx * 64 * sizeof(KT) > 0x7fffffffu ||
+      !(qkv || qp) || !kcache || !vcache || !part || !o)
+    return hipErrorInvalidValue;
+  if (qp && (!qp->part || qp->S < 1 || qp->M != B || (size_t)qp->S * B * 3 * d * 4 > 0x7fffffffu))
     return hipErrorInvalidValue;
   const int maxc = (ctx + CHUNK - 1) / CHUNK;
-  hipLaunchKernelGGL(k_attn_decode_wide<KT>, dim3(maxc, H, B), dim3(256), 0, st, src, qkv, d, H, ctx, kcache, vcache,
-                     part, maxc);
+  KT* kc = const_cast<KT*>(kcache);
+  KT* vc = const_cast<KT*>(vcache);
+  if (qp)
+    hipLaunchKernelGGL((k_attn_decode_wide<KT, true>), dim3(maxc, H, B), dim3(256), 0, st, src, qkv, d, H, ctx, kc, vc,
+                       part, maxc, *qp);
+  else
+    hipLaunchKernelGGL((k_attn_decode_wide<KT, false>), dim3(maxc, H, B), dim3(256), 0, st, src, qkv, d, H, ctx, kc,
+                       vc, part, maxc, QkvParts{});
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !combine) return e;
   return launch_attn_decode_combine(st, src, B, d, H, ctx, part, CHUNK, maxc, o);
 }
 
 template hipError_t launch_attn_decode_wide<float>(hipStream_t, RowSrc, const float*, int, int, int, int,
-                                                   const float*, const float*, float*, float*, bool);
+                                                   const float*, const float*, float*, float*, bool, const QkvParts*);
 template hipError_t launch_attn_decode_wide<bf16_t>(hipStream_t, RowSrc, const float*, int, int, int, int,
-                                                    const bf16_t*, const bf16_t*, float*, float*, bool);
+                                                    const bf16_t*, const bf16_t*, float*, float*, bool, const QkvParts*);
 
 }  // namespace fh

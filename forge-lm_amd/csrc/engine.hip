@@ -475,8 +475,9 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     const int L = s->d.n_layers;
     LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
     if (B > 4 && D == 64 * H && C <= 4 * kAttnDecodeChunk) {
-      // the attention combine is folded into the attn.proj GEMM's operand load
-      // (9 launches per layer); folding the mlp.fc reduction into mlp.proj's
+      // the qkv reduction and KV store are folded into the attention and the
+      // attention combine into the attn.proj GEMM's operand load (8 launches per
+      // layer); folding the mlp.fc reduction into mlp.proj's
       // operand load was measured slower (each mlp.proj block re-reads 8 partials
       // of its A chunk: 19 MB per layer)
       const int cus = s->ctx->props.multiProcessorCount;
@@ -486,8 +487,9 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
         int S = 0;
         LAUNCH(launch_gemm_mfma_split<WT>(st, s->xn, B, D, s->wt<WT>(s->idx_blk(l, 2)), 3 * D, s->part,
                                           s->part_floats, cus, &S));
-        LAUNCH(launch_epilogue_qkv<WT>(st, s->part, S, B, D, s->v(s->idx_blk(l, 3)), s->qkv, src, 1, H, C, kc, vc));
-        LAUNCH(launch_attn_decode_wide<WT>(st, src, s->qkv, B, D, H, C, kc, vc, s->apart, s->o, false));
+        // the attention sums the qkv partials itself and stores the new K/V rows
+        const QkvParts qp{s->part, S, B, s->v(s->idx_blk(l, 3))};
+        LAUNCH(launch_attn_decode_wide<WT>(st, src, nullptr, B, D, H, C, kc, vc, s->apart, s->o, false, &qp));
         AOperand ao{};
         ao.kind = AOP_ATTN;
         ao.apart = s->apart;

@@ -84,10 +84,19 @@ hipError_t launch_attn_decode_combine(hipStream_t st, RowSrc src, int B, int d, 
 // The same decode attention for head_dim 64 (attn_decode.hip): 256-key chunks,
 // one 1 KB request per 4 K or V rows.  part must hold B*H*ceil(ctx/256)*66 floats.
 // Without `combine` only the chunk partials are written (the consumer combines).
+// With qp, q comes from the qkv projection's split-K partials (summed with the
+// bias as k_epilogue_qkv does; qkv is not read) and the new K/V row of each
+// sequence is written into the caches by the block that attends over it.
 constexpr int kAttnDecodeChunk = 256;
+struct QkvParts {
+  const float* part;  // [S][M][3d]
+  int S, M;
+  const float* bias;  // [3d] or null
+};
 template <typename KT>
 hipError_t launch_attn_decode_wide(hipStream_t st, RowSrc src, const float* qkv, int B, int d, int H, int ctx,
-                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine = true);
+                                   const KT* kcache, const KT* vcache, float* part, float* o, bool combine = true,
+                                   const QkvParts* qp = nullptr);
 
 // Tied head for B rows: logits[b, v] = dot(xn[b,:], E[v,:]).
 template <typename WT>
