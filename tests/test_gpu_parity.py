@@ -559,3 +559,22 @@ def test_batched_decode_fused_epilogues(fhp, oracle, backend, B, dtype):
                 break
             assert ids[b][n] == rids[n], (b, n)
     m.dispose()
+
+
+def test_batched_decode_past_four_attention_chunks(fhp, oracle, backend):
+    # more than 4 rows and a context above 1024 positions: the attention chunks
+    # are combined by their own kernel (the attn.proj operand load combines at
+    # most 4) while the split-K reductions stay fused with the KV store and the
+    # LayerNorms; positions 1030..1049 span five 256-key chunks
+    shape = (512, 1100, 128, 2, 2)
+    B, P, NEW = 6, 1030, 20
+    m, oc, w = make_model(fhp, oracle, backend, shape, 41, batch=B)
+    r = fhp.TrainingRandom(19)
+    prompts = np.stack([r.ids(shape[0], P) for _ in range(B)])
+    ids, lg = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
+    oracle.set_threads(8)
+    for b in range(B):
+        rids, rlg = oracle.generate(oc, w, prompts[b], NEW, return_logits=True)
+        np.testing.assert_array_equal(ids[b], rids)
+        assert rel_err(lg[b], rlg) <= TOL_F32
+    m.dispose()
