@@ -7,7 +7,10 @@
 // its 4 waves reads 64 K and 64 V rows with one 1 KB load per 4 rows (lane l:
 // dims 4*(l % 16) .. +3 of row 4i + l / 16), so every request is a contiguous
 // 1 KB; the block's partial (o[64], max, sum) is combined with the other
-// chunks' by k_attn_decode_combine.  Memory bound: 2 * nkeys * 256 bytes per (b, h).
+// chunks' by k_attn_decode_combine, or by the attn.proj GEMM as it loads its
+// operand.  In batched decode the kernel also takes q from the qkv projection's
+// split-K partials and the block over the new position stores its K/V rows
+// before reading the cache.  Memory bound: 2 * nkeys * 256 bytes per (b, h).
 #include "kernels.hpp"
 
 #include <math.h>
