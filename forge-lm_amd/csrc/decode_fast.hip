@@ -1423,8 +1423,11 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   ctx = d.context_length;
   C = KPB;
   blocks = NB;
+  // every data wave needs at least one vocabulary row of the head (its first
+  // rows are requested unconditionally): V / NB >= NDW
   const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == kD && H == kH && V % NB == 0 &&
-                        V / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH && compute_units >= NB &&
+                        V / NB >= NDW && V / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH &&
+                        compute_units >= NB &&
                         PH * L + 1 <= TAGS;
   if (!shape_ok) return FH_OK;
   int occ = 0;

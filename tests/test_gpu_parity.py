@@ -121,6 +121,22 @@ def test_fused_greedy_without_dump_matches_dump_run(fhp, oracle, backend):
     m.dispose()
 
 
+@pytest.mark.parametrize("V", [512, 768, 2816])
+def test_d768_small_vocab_greedy_matches_oracle(fhp, oracle, backend, V):
+    """Vocabularies below, at and above three head rows per block of the fused step
+    (512 takes the generic kernels; 768 and 2816 the fused step, 2816 with rows split
+    unevenly over its data waves), with and without the logits dump."""
+    shape = (V, 1024, 768, 2, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 21)
+    prompt = fhp.TrainingRandom(3).ids(V, 30)
+    ids, lg = fhp.Sampler.generate(m, prompt, 40, 0.0, 0, None, return_logits=True)
+    rids, rlg = oracle.generate(oc, w, prompt, 40, return_logits=True)
+    np.testing.assert_array_equal(ids, rids)
+    assert rel_err(lg, rlg) <= TOL_F32
+    np.testing.assert_array_equal(fhp.Sampler.generate(m, prompt, 40, 0.0, 0, None), rids)
+    m.dispose()
+
+
 def test_forward_last_batch_matches_oracle(fhp, oracle, backend):
     shape = (16384, 1024, 768, 12, 12)
     m, oc, w = make_model(fhp, oracle, backend, shape, 77, batch=2)
