@@ -10,9 +10,10 @@
 //   A  LN1 + QKV: the 192 q/k/v columns of head h are computed by blocks of
 //      XCD h % 8 only, so q/k/v reach that head's attention blocks through the
 //      XCD's own L2; the new K/V row goes into the cache
-//   B  attention of head h by blocks of XCD h % 8: 64 keys per data wave
-//      (lane = key for the scores, lane = dim for P.V), 192 keys per block;
-//      a head spanning several blocks is combined by its first block
+//   B  attention of head h by blocks of XCD h % 8: 32 keys per data wave
+//      (lane l: dims 4*(l % 16) .. +3 of every fourth key), 96 keys per block,
+//      each block publishing a partial (o, max, sum); every block of the XCD
+//      combines the partials of all the XCD's heads itself
 //   C  attn.proj columns + residual -> x2
 //   D  LN2 + mlp.fc columns + GELU -> h
 //   E  mlp.proj columns + residual -> x
