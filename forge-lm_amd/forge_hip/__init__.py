@@ -12,4 +12,3 @@ from .sampler import Sampler  # noqa: F401
 from .checkpoint import Checkpoint  # noqa: F401
 from .chat import Chat  # noqa: F401
 from .tensor_backend import HipTensorBackend, Tensor  # noqa: F401
-from .training import AdamW, Parameters, TrainableGptModel  # noqa: F401
