@@ -13,10 +13,15 @@ every weight once + the KV rows read and written + two embedding rows; one
 fused launch runs all 255 cached greedy steps) over its duration, timed with
 HIP events on the session stream inside the library.
 cpu_baseline: the oracle's restatement of the reference CPU algorithm
-(full-window recompute per token, Sampler.Generate semantics) on this host,
-on the first tokens of the same workload.
+(full-window recompute per token, Sampler.Generate semantics) on this host's
+cores (up to the 16 CPUs a GPU job is given on this pool), timed on the first
+tokens of the same workload and extrapolated to the whole run by the FLOPs of
+each step's window.
 
-The other configurations are separate lines, one per run:
+The default line also carries the rest of BASELINE's metric, measured in the
+same run: "bs32_decode" (config 4, batch 32) and "prefill" (config 5, bf16
+prefill), each with its own roofline (--no-extra leaves them out).  Each
+configuration also runs alone:
   --workload c3  sampling path (T 0.7, top-k 30, penalty 1.1, no-repeat 4-gram),
                  prompt 32 + 512 tokens; roofline over one decode step
   --workload c4  batch 32, prompts 512 (PCG32 seeds 42 + b) + 512 greedy;
@@ -26,13 +31,14 @@ The other configurations are separate lines, one per run:
                  re-prefills the full window); value = prefill tok/s, roofline
                  = prefill FLOPs / prefill time against the bf16 MFMA peak
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--workload c2|c3|c4|c5]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--workload c2|c3|c4|c5]
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
 import sys
 import time
 
@@ -93,12 +99,38 @@ def bf16_round(x):
     return u.astype(np.uint32).view(np.float32)
 
 
+def window_flops(c, T: int) -> float:
+    """FLOPs of one reference decode step (Sampler.Generate recomputes the whole
+    window of T rows, GptModel.cs:202-222): every linear layer and the tied head
+    over T rows, plus QK^T and PV over the full T x T score matrix of every head."""
+    d, L, V = c["d_model"], c["n_layers"], c["vocab_size"]
+    return 2.0 * T * (L * 12 * d * d + V * d) + 4.0 * L * d * T * T
+
+
+def host_cpu():
+    """(logical CPUs, CPU model name) of this host."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return os.cpu_count() or 1, model
+
+
 def cpu_baseline(name: str, w: dict, prompts, gpu_ids, budget_tokens: int):
-    """The oracle (reference CPU algorithm, full-window recompute) on a bounded sample of the workload."""
+    """The oracle (reference CPU algorithm, full-window recompute) on a bounded sample
+    of the workload, extrapolated to the whole workload by window FLOPs."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
-    threads = min(16, os.cpu_count() or 1)
+    nproc, model_name = host_cpu()
+    # a GPU job on this pool is given 16 CPUs whatever the host shows (more threads
+    # would only contend with other jobs' threads)
+    threads = min(16, nproc)
     O.set_threads(threads)
     oc = O.Config(*[w["shape"][k] for k in DIMS])
     wt = O.init_weights(oc, 1234)
@@ -114,12 +146,21 @@ def cpu_baseline(name: str, w: dict, prompts, gpu_ids, budget_tokens: int):
     t0 = time.perf_counter()
     ids = O.generate(oc, wt, prompt, n, kv_cached=False, **kw)
     dt = time.perf_counter() - t0
+    # step j of the workload recomputes a window of min(P + j, ctx) rows; the sample
+    # ran steps 0..n-1, the workload runs w["new"] steps per sequence, batch of them
+    ctx = w["shape"]["context_length"]
+    cost = [window_flops(w["shape"], min(w["prompt"] + j, ctx)) for j in range(w["new"])]
+    full_s = dt * sum(cost) / sum(cost[:n]) * w["batch"]
     what = "sequence 0 of %d, " % w["batch"] if w["batch"] > 1 else ""
     out = {
-        "value": n / dt, "unit": "tok/s", "cores": threads, "kind": "port",
+        "value": w["batch"] * w["new"] / full_s, "unit": "tok/s", "cores": threads, "kind": "port",
+        "host_cpus": nproc, "cpu_model": model_name,
         "sample": (f"reference CPU algorithm (C++ restatement, full-window recompute per token as "
-                   f"Sampler.Generate does) on the {name.upper()} weights and prompt: {what}first {n} of "
-                   f"{w['new']} tokens, {dt:.1f} s, {threads} threads"),
+                   f"Sampler.Generate does) on the {name.upper()} weights and prompt: {what}steps 0..{n - 1} "
+                   f"of {w['new']} ran in {dt:.1f} s on {threads} threads ({n / dt:.3g} tok/s); value = the "
+                   f"whole workload ({w['batch']} x {w['new']} tokens) extrapolated by the FLOPs of each "
+                   f"step's window: {full_s:.0f} s"),
+        "sample_tok_s": n / dt,
         "ids_match_gpu": bool((np.asarray(ids) == np.asarray(gpu0)[:n]).all()),
     }
     if name == "c5":
@@ -146,27 +187,34 @@ def copy_calibration(mib: int, reps: int) -> dict:
             "read_plus_write_GBs": round(2 * nbytes / best / 1e6, 1)}
 
 
+TRAFFIC_PROFILE = os.path.join("profiles", "decode_step_c2_traffic.md")
+
+
 def profiled_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "decode_step_c2_traffic.md")
+    """(HBM bytes per launch of `kernel`, what build they were counted on) from the
+    committed counter summary (two rocprofv3 --pmc runs; the counters cannot be read
+    inside this run), or (None, None)."""
+    value, build = None, None
     try:
-        with open(path) as f:
+        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:") and kernel in line:
-                    return int(line.split(":", 1)[1].split()[0])
+                    value = int(line.split(":", 1)[1].split()[0])
+                elif line.startswith("measured_on:"):
+                    build = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return None
+    return value, build
 
 
-def run_workload(name: str, args) -> dict:
+def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: int = 0) -> dict:
     import numpy as np
     import forge_hip as fhp
 
     w = dict(WORKLOADS[name])
-    if args.new:
-        w["new"] = args.new
-        w["desc"] += f" (shortened to {args.new} new tokens)"
+    if new:
+        w["new"] = new
+        w["desc"] += f" (shortened to {new} new tokens)"
     c = w["shape"]
     cfg = fhp.ModelConfig(**c)
     be = fhp.HipBackend(0)
@@ -180,11 +228,11 @@ def run_workload(name: str, args) -> dict:
             return fhp.Sampler.generate(model, prompts, NEW, T, k, fhp.Random(seed), None, pen, ng)
         return fhp.Sampler.generate(model, prompts, NEW, 0.0, 0, None)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         ids = one()
     decode_ms, prefill_ms, timings = [], [], []
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         ids = one()
         t = fhp.Sampler.last_timing
         timings.append(t)
@@ -201,10 +249,10 @@ def run_workload(name: str, args) -> dict:
         raise SystemExit("--new must be at least 2 for a decode workload (token 0 comes from the prefill)")
     avg_step_s = dec_s / n_dec if n_dec else 0.0
     ctx = c["context_length"]
-    value = args.steps * B * NEW / wall
+    value = steps * B * NEW / wall
     out = {
-        "metric": None, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3), "higher_is_better": True,
+        "metric": None, "value": round(value, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(wall / steps * 1e3, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": w["dtype"],
         "data": "synthetic (random-init weights from new Random(1234); PCG32 prompt ids, seed 42 + sequence)",
         "config": {"workload": w["desc"], "batch": B, "prompt_len": P, "new_tokens": NEW},
@@ -226,26 +274,34 @@ def run_workload(name: str, args) -> dict:
                          "flops_per_launch": flops, "launch_us": round(pre_s * 1e6, 1)},
         })
         # the timed unit is one prefill forward; value is its token rate
-        out["steps"] = args.steps
+        out["steps"] = steps
     else:
         # decode step n attends P+n keys (positions 0..P+n-1 plus itself), n = 1..NEW-1
         attended = float(np.mean([min(P + n, ctx) for n in range(1, NEW)]))
         step_bytes = decode_bytes_per_step(c, attended, batch=B)
         achieved = step_bytes / avg_step_s / 1e9
-        fused = name == "c2" and os.environ.get("FORGE_HIP_FUSED_DECODE", "1") != "0"
-        kernel = "k_decode_step<768>" if fused else "decode step graph (generic kernels)"
-        tokens_per_launch = n_dec if fused else 1
+        rt = timings[-1]["route"]
+        persistent = rt == fhp._native.FH_ROUTE_FUSED_STEP and not w["sampling"]
+        if rt & fhp._native.FH_ROUTE_FUSED_STEP:
+            kernel = ("k_decode_step<768>" if persistent else
+                      "k_decode_step<768> + k_sample_row (one launch of each per sampled token)")
+        else:
+            kernel = "decode step graph (generic kernels)"
+        tokens_per_launch = n_dec if persistent else 1
+        traffic, traffic_build = profiled_traffic(kernel) if (persistent and name == "c2") else (None, None)
         out.update({
             "decode_tok_s": round(B * n_dec / dec_s, 2),
             "decode_us_per_step": round(avg_step_s * 1e6, 2),
             "prefill_tok_s": round(B * P / pre_s, 2),
             "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(achieved / HBM_PEAK_GBS, 4),
-                         "traffic": profiled_traffic(kernel) if fused else None,
+                         "traffic": traffic,
                          "kernel": kernel, "tokens_per_launch": tokens_per_launch,
                          "bytes_per_launch": int(step_bytes * tokens_per_launch),
                          "launch_us": round(avg_step_s * tokens_per_launch * 1e6, 2)},
         })
+        if traffic is not None:
+            out["roofline"]["traffic_source"] = f"{TRAFFIC_PROFILE} (counted on {traffic_build})"
         if name == "c2":
             out["metric"] = "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)"
             out["decode_us_per_token"] = out.pop("decode_us_per_step")
@@ -254,7 +310,7 @@ def run_workload(name: str, args) -> dict:
         else:
             out["metric"] = "decode tok/s, Forge-98M shape fp32 bs32 (prompt 512 + 512 greedy)"
     out["device"] = be.device_name
-    if not args.no_cpu:
+    if with_cpu:
         budget = args.cpu_tokens if args.cpu_tokens else {"c2": 96, "c3": 96, "c4": 12, "c5": 2}[name]
         out["cpu_baseline"] = cpu_baseline(name, w, prompts, ids, budget)
     model.dispose()
@@ -271,6 +327,8 @@ def main():
     ap.add_argument("--new", type=int, default=0,
                     help="generate this many tokens instead of the workload's count (short profiling runs)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="C2 only: leave out the bs32 decode (C4) and prefill (C5) sub-objects")
     ap.add_argument("--cpu-tokens", type=int, default=0,
                     help="tokens of the workload the CPU baseline runs (default: about 10-25 s on 16 cores)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -284,7 +342,16 @@ def main():
     if args.copy_calibration:
         print(json.dumps(copy_calibration(args.copy_calibration, max(1, args.steps))), flush=True)
         return
-    print(json.dumps(run_workload(args.workload, args)), flush=True)
+    line = run_workload(args.workload, args, args.steps, args.warmup, not args.no_cpu, args.new)
+    if args.workload == "c2" and not args.no_extra and not args.new:
+        # the rest of the metric ("bs1/bs32 ... prefill tok/s"), two timed passes each
+        keep = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
+                "decode_tok_s", "decode_us_per_step", "prefill_tok_s", "decode_tok_s_reprefill",
+                "reprefill_ms_per_step", "whole_job_tok_s", "metric")
+        for key, wl in (("bs32_decode", "c4"), ("prefill", "c5")):
+            sub = run_workload(wl, args, 2, 1, False)
+            line[key] = {k: sub[k] for k in keep if k in sub}
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -71,9 +71,11 @@ __device__ __forceinline__ bool err_set(int* err) {
 }
 // The first failing wait records where it was: 1 << 31 | wait << 24 | layer << 16 | block
 // (waits: 1 x, 2 q/k/v, 3 attention partials, 5 attn.proj partials, 6 x2, 7 h,
-// 8 mlp.proj partials, 9 final x, 10 argmax; 4 is not used).
-// A wait that gives up because another block already failed records nothing.
-enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX };
+// 8 mlp.proj partials, 9 final x, 10 argmax; 4 is not used), or which check
+// failed (11 a token id outside [0, V), 12 two blocks of the launch on the same
+// (XCD, slot)).  A wait that gives up because another block already failed
+// records nothing.
+enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX, W_TOK, W_XCD };
 __device__ __forceinline__ int err_code(int wait, int l) {
   return (int)(0x80000000u | ((unsigned)wait << 24) | ((unsigned)(l & 0xff) << 16) | blockIdx.x);
 }
@@ -180,14 +182,16 @@ struct KParams {
   float* logits;
   int* out_ids;
   int* out_counts;
-  uint2* uc;          // uncached pairs (Xu), then the argmax records
+  uint2* uc;          // uncached pairs (Xu), then the argmax records, then the slot claims
   int uc_bytes;
   int off_amax;       // byte offset of the argmax records in uc
+  int off_claim;      // byte offset of the (XCD, slot) claim words in uc
   uint2* xl;          // per-XCD pairs (Xl), ordinary device memory
   int xl_bytes;
   unsigned* launch;   // launch counter
   int* err;
   int V, ctx, L, max_new, eos, greedy;
+  int R;              // vocabulary rows per block of the head: ceil(V / 256), rows >= V are skipped
   int nsteps;         // decode steps of this launch (greedy: the argmax feeds the next step)
   int* tokens_out;    // same buffer as src.tokens, written by the greedy argmax
   int* step_out;      // same word as src.step
@@ -611,6 +615,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     if (l > 0 && !dead && !gather<D>(ncl, r.xl0 + XL::X, tb - PH + 7, sh.xres, p.err, err_code(W_X, l), D, &np[0]))
       fail();
     __syncthreads();
+    if (it == 0 && sh.fail) dead = true;  // a check at the kernel's start failed
     TM(0);
     if (it == r.trace_it + 1) trace_mark(p.trace, 9);
     // Every phase whose data waves publish and then request tiles has a
@@ -732,10 +737,10 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       const unsigned tH = tbase + PH * p.L;
       if (!dead) {
         // this block's logits (for a host-side sampler) and its argmax record
-        const int R = p.V / NB;
+        const int R = p.R;
         float best = -INFINITY;
         int bi = 0x7fffffff;
-        if (lane < R) {
+        if (lane < R && r.blk * R + lane < p.V) {
           const float sv = sh.hval[lane];
           const int v = r.blk * R + lane;
           if (!p.greedy) p.logits[v] = sv;
@@ -758,6 +763,9 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
         int bi;
         if (!gather_argmax<NB>(ncu, p.off_amax, tH, best, bi, p.err, err_code(W_AMAX, 0))) {
           fail();
+        } else if ((unsigned)bi >= (unsigned)p.V) {  // no finite logit: no id to record or feed back
+          if (lane == 0) raise_err(p.err, err_code(W_TOK, 0));
+          fail();
         } else {
           const int n = r.n0 + t;
           if (r.blk == 0 && lane == 0 && p.greedy) {
@@ -769,7 +777,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
           if (thead) trace_mark(p.trace, 18);
           if (next) {
             // x of the next token = tok_emb[id] + pos_emb[pos + 1]
-            const int id = (unsigned)bi < (unsigned)p.V ? bi : 0;
+            const int id = bi;
             const float* te = p.tok + (size_t)id * D;
             const float* pe = p.pos + (size_t)(r.pos0 + t + 1) * D;
 #pragma unroll
@@ -1153,18 +1161,24 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
     site(std::integral_constant<int, S_EEND>());
     if (run && l == p.L - 1) {
       // ---- head of token t: LN_f + tied projection over this block's vocab rows ----
-      const int R = p.V / NB;  // rows per block; data wave w takes rows w, w+3, ...
+      // block b owns rows [b*R, b*R + R) below V (the last blocks hold fewer, or
+      // none, when V is not a multiple of 256); data wave w takes rows w, w+3, ...
+      const int R = p.R;
       constexpr int HG = FH_HG;  // rows per wave in flight
-      const float* E = p.tok + (size_t)r.blk * R * D;
-      const int nrow = (R - w + NDW - 1) / NDW;
+      const int row0 = r.blk * R;
+      const int nrow = (max(0, min(R, p.V - row0)) - w + NDW - 1) / NDW;  // may be <= 0
+      // row u of this wave, clamped into the table (a wave without rows re-reads a
+      // valid row and computes nothing)
+      auto head_row = [&](int u) {
+        return p.tok + (size_t)min(max(row0 + w + NDW * min(u, nrow - 1), 0), p.V - 1) * D;
+      };
       // the first rows are requested before the final x arrives
       float4 rh[HG * KC];
 #pragma unroll
       for (int u = 0; u < HG; u++) {
-        const int row = w + NDW * min(u, nrow - 1);
+        const float* e = head_row(u);
 #pragma unroll
-        for (int c = 0; c < KC; c++)
-          rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+        for (int c = 0; c < KC; c++) rh[u * KC + c] = *reinterpret_cast<const float4*>(e + c * 256 + lane * 4);
       }
       __syncthreads();  // the final x is in xres
       dead = sh.fail != 0;
@@ -1183,10 +1197,9 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
           float4 nx[HG * KC];
 #pragma unroll
           for (int u = 0; u < HG; u++) {
-            const int row = w + NDW * min(g + HG + u, nrow - 1);
+            const float* e = head_row(g + HG + u);
 #pragma unroll
-            for (int c = 0; c < KC; c++)
-              nx[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+            for (int c = 0; c < KC; c++) nx[u * KC + c] = *reinterpret_cast<const float4*>(e + c * 256 + lane * 4);
           }
 #pragma unroll
           for (int u = 0; u < HG; u++) {
@@ -1233,7 +1246,6 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // every tile and bias depends on (XCD, slot): they are stored under the
   // virtual block id vb; the head rows are indexed by blk
   r.vb = r.slot * NX + r.xcd;
-  if (tid == 0) sh.fail = 0;
   if (tid < 32) sh.trd[tid] = 0ull;
   if (p.trace && tid == NT - 64) p.trace[r.blk * TRACE_PER + 12] = (unsigned long long)r.xcd;
   r.tag0 = __hip_atomic_load(p.launch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * TAGS;
@@ -1246,7 +1258,24 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   r.pos = r.pos0;
   r.nk = r.pos0 + 1;
   int tokid = p.src.tokens[p.src.tok_off + r.n0];
-  if ((unsigned)tokid >= (unsigned)p.V) tokid = 0;
+  bool bad = false;
+  if ((unsigned)tokid >= (unsigned)p.V) {  // never read outside the table: report it and run no step
+    tokid = 0;
+    bad = true;
+    if (tid == 0) raise_err(p.err, err_code(W_TOK, 0));
+  }
+  // Every (XCD, slot) must be taken by exactly one block of the launch: each block
+  // swaps this launch's mark into its slot's claim word (uncached, so the swap is
+  // device-wide) and fails fast if a block of the same launch got there first.
+  if (tid == 0) {
+    unsigned* claim = reinterpret_cast<unsigned*>(reinterpret_cast<char*>(p.uc) + p.off_claim) + r.vb;
+    const unsigned mark = r.tag0 | 1u;
+    if (__hip_atomic_exchange(claim, mark, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == mark) {
+      raise_err(p.err, err_code(W_XCD, 0));
+      bad = true;
+    }
+  }
+  if (tid == 0) sh.fail = bad ? 1 : 0;  // read by every wave after its first barrier
   r.xl = p.xl + (size_t)r.xcd * XL::STRIDE;
   r.xl0 = r.xcd * XL::STRIDE;
   // qkv columns: the XCD's heads h = xcd + 8j (j < nh) own columns
@@ -1367,7 +1396,9 @@ constexpr int kD = 768, kH = 12;
 using S768 = Shape<kD, kH>;
 
 size_t uc_pairs_bytes(int D) { return (size_t)Xu<kD>::NPAIR * sizeof(uint2) * (D / kD); }
-size_t uc_total_bytes(int D) { return (uc_pairs_bytes(D) + 255) / 256 * 256 + (size_t)NB * sizeof(uint4); }
+size_t uc_amax_off(int D) { return (uc_pairs_bytes(D) + 255) / 256 * 256; }
+size_t uc_claim_off(int D) { return uc_amax_off(D) + (size_t)NB * sizeof(uint4); }
+size_t uc_total_bytes(int D) { return uc_claim_off(D) + (size_t)NB * sizeof(unsigned); }
 
 // Host maps, all per virtual block vb = slot * 8 + XCD:
 //   q  qkv columns by XCD head ownership          f  mlp.fc columns: the XCD's h slice
@@ -1424,10 +1455,9 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   ctx = d.context_length;
   C = KPB;
   blocks = NB;
-  // every data wave needs at least one vocabulary row of the head (its first
-  // rows are requested unconditionally): V / NB >= NDW
-  const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == kD && H == kH && V % NB == 0 &&
-                        V / NB >= NDW && V / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH &&
+  // the head gives each block ceil(V / 256) <= 64 vocabulary rows
+  const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == kD && H == kH &&
+                        (V + NB - 1) / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH &&
                         compute_units >= NB &&
                         PH * L + 1 <= TAGS;
   if (!shape_ok) return FH_OK;
@@ -1559,12 +1589,14 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.out_counts = s.out_counts;
   k.uc = reinterpret_cast<uint2*>(uc);
   k.uc_bytes = (int)xch_bytes;
-  k.off_amax = (int)((uc_pairs_bytes(D) + 255) / 256 * 256);
+  k.off_amax = (int)uc_amax_off(D);
+  k.off_claim = (int)uc_claim_off(D);
   k.xl = reinterpret_cast<uint2*>(xl);
   k.xl_bytes = (int)xl_bytes;
   k.launch = reinterpret_cast<unsigned*>(ctl);
   k.err = reinterpret_cast<int*>(ctl) + 16;
   k.V = V;
+  k.R = (V + NB - 1) / NB;
   k.ctx = ctx;
   k.L = L;
   k.max_new = s.max_new;

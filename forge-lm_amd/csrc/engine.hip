@@ -17,6 +17,7 @@
 // HIP graph and replayed.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -186,6 +187,7 @@ struct GraphKey {
 struct CachedGraph {
   GraphKey key;
   hipGraphExec_t exec = nullptr;
+  int route = 0;  // FH_ROUTE_* bits of the decode step the graph holds
 };
 
 namespace {
@@ -254,6 +256,7 @@ struct fh_session {
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   double t_prefill = 0, t_decode = 0;
   int n_cached = 0, n_reprefill = 0;
+  int route = 0;  // FH_ROUTE_* bits of the decode steps enqueued since the last generate began
 
   template <typename T>
   const T* w(size_t i) const {
@@ -473,8 +476,10 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     // each split-K reduction also does the work of the kernel after it; the last
     // mproj reduction applies LN_f, so xn holds the head's input on return
     const int L = s->d.n_layers;
+    s->route |= FH_ROUTE_FUSED_EPILOGUES;
     LAUNCH(launch_layernorm(st, s->x, B, B, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
     if (B > 4 && D == 64 * H && C <= 4 * kAttnDecodeChunk) {
+      s->route |= FH_ROUTE_ATTN_IN_PROJ;
       // the qkv reduction and KV store are folded into the attention and the
       // attention combine into the attn.proj GEMM's operand load (8 launches per
       // layer); folding the mlp.fc reduction into mlp.proj's
@@ -534,6 +539,7 @@ int enqueue_layers_decode(fh_session* s, RowSrc src) {
     }
     return FH_OK;
   }
+  s->route |= FH_ROUTE_UNFUSED;
   for (int l = 0; l < s->d.n_layers; l++) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
@@ -633,6 +639,7 @@ int enqueue_decode_step(fh_session* s, const StepPlan& p) {
     // greedy without repetition controls or a logits dump: the argmax runs
     // inside the decode kernel and no sampler launch follows
     const bool greedy = fused_greedy(s, p.opts);
+    s->route |= FH_ROUTE_FUSED_STEP;
     int rc = s->fast.enqueue(st, fused_step(s, p, greedy ? 1 : 0, 1));
     if (rc != FH_OK) return set_err(rc, "fused decode step launch failed: %s", hipGetErrorString(hipGetLastError()));
     if (greedy) return FH_OK;
@@ -663,7 +670,9 @@ int capture(fh_session* s, CachedGraph& g, const GraphKey& key, F&& enqueue) {
   drop_graph(g);
   hipStream_t st = s->ctx->stream;
   HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  s->route = 0;
   int rc = enqueue();
+  g.route = s->route;
   hipGraph_t graph = nullptr;
   hipError_t e = hipStreamEndCapture(st, &graph);
   if (rc != FH_OK) {
@@ -991,9 +1000,11 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
   sp->vc = vc;
   const size_t rows = (size_t)B * C;
   const int maxc = (C + 63) / 64;
-  // split-K partials: the GEMV path (up to 64 splits of 4 rows) and the MFMA
-  // GEMM's small-M split (up to 8 splits of 64 rows of the widest layer)
-  sp->part_floats = std::max((size_t)64 * 4 * 4 * D, (size_t)8 * 64 * 4 * D);
+  // split-K partials: the GEMV path (up to 64 splits of 4 rows), the MFMA GEMM's
+  // small-M split (up to 8 splits of 64 rows of the widest layer), and at least
+  // one unsplit product of every decode row (the batched decode's split GEMMs need
+  // B x 3D; the split count shrinks to what fits)
+  sp->part_floats = std::max({(size_t)64 * 4 * 4 * D, (size_t)8 * 64 * 4 * D, (size_t)B * 4 * D});
   if ((rc = dev_alloc(&sp->x, rows * D)) || (rc = dev_alloc(&sp->x2, rows * D)) || (rc = dev_alloc(&sp->xn, rows * D)) ||
       (rc = dev_alloc(&sp->qkv, rows * 3 * D)) || (rc = dev_alloc(&sp->o, rows * D)) ||
       (rc = dev_alloc(&sp->h, rows * 4 * D)) || (rc = dev_alloc(&sp->part, sp->part_floats)) ||
@@ -1302,6 +1313,7 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   s->dump = saved_dump;
   s->uniforms = saved_u;
   if (rc != FH_OK) return rc;
+  s->route = g.persistent ? FH_ROUTE_FUSED_STEP : (g.n_dec > 0 ? s->g_decode.route : 0);
   g.active = true;
   return FH_OK;
 }
@@ -1356,10 +1368,18 @@ static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, flo
   if (s->use_fast() && g.n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
     s->fast.reset();
     g.active = false;
+    const unsigned what = (wait_code >> 24) & 0x7f;
+    if (what == 11)
+      return set_err(FH_ERR_HIP, "fused decode step: a token id outside [0, VocabSize) (results discarded)");
+    if (what == 12)
+      return set_err(FH_ERR_HIP,
+                     "fused decode step: two blocks of one launch ran on the same XCD slot (block %u; the "
+                     "dispatcher no longer deals blocks round-robin over the XCDs; results discarded)",
+                     wait_code & 0xffff);
     return set_err(FH_ERR_HIP,
                    "fused decode step: a hand-off wait exceeded its spin limit (wait %u, layer %u, block %u; "
                    "results discarded)",
-                   (wait_code >> 24) & 0x7f, (wait_code >> 16) & 0xff, wait_code & 0xffff);
+                   what, (wait_code >> 16) & 0xff, wait_code & 0xffff);
   }
   // a sequence without EOS so far has produced every step enqueued
   for (int b = 0; b < B; b++)
@@ -1441,6 +1461,12 @@ int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n) {
   if (!s->fast.trace) return set_err(FH_ERR_STATE, "tracing is off (set FORGE_HIP_TRACE=1 before creating the session)");
   HIP_TRY(hipStreamSynchronize(s->ctx->stream));
   HIP_TRY(hipMemcpy(out, s->fast.trace, sizeof(unsigned long long) * std::min(n, 256 * 64), hipMemcpyDeviceToHost));
+  return FH_OK;
+}
+
+int fh_last_route(fh_session* s, int32_t* route) {
+  if (!s || !route) return set_err(FH_ERR_INVALID, "null argument");
+  *route = s->route;
   return FH_OK;
 }
 

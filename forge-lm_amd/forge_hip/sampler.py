@@ -74,8 +74,10 @@ class Sampler:
         nc, nr = ctypes.c_int32(), ctypes.c_int32()
         N.check(N.lib().fh_last_timing(model.handle, ctypes.byref(pre), ctypes.byref(dec), ctypes.byref(nc),
                                        ctypes.byref(nr)))
+        route = ctypes.c_int32()
+        N.check(N.lib().fh_last_route(model.handle, ctypes.byref(route)))
         Sampler.last_timing = {"prefill_ms": pre.value, "decode_ms": dec.value, "cached_steps": nc.value,
-                               "reprefill_steps": nr.value}
+                               "reprefill_steps": nr.value, "route": route.value}
         if uniforms is not None:
             rng.skip(int(counts[0]) if B == 1 else B * max_new_tokens)
         ids = [out[b, :counts[b]].copy() for b in range(B)]

@@ -182,6 +182,16 @@ int fh_generate_next(fh_session* s, int steps, const double* uniforms, int32_t* 
 int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t* cached_steps,
                    int32_t* reprefill_steps);
 
+/* Which kernels ran the cached decode steps of the last fh_generate /
+ * fh_generate_begin (0 when it had none): a diagnostic for tests, like the
+ * reference CUDA backend's test-only call counters (FusedAttentionCallCount and
+ * the others, src/LLM.Core/Tensor/Cuda/CudaBackend.cs:257-270). */
+#define FH_ROUTE_FUSED_STEP 1       /* the persistent batch-1 decode kernel */
+#define FH_ROUTE_FUSED_EPILOGUES 2  /* split-K reductions fused with the KV store and LayerNorms */
+#define FH_ROUTE_ATTN_IN_PROJ 4     /* + attention chunks combined in attn.proj's operand load */
+#define FH_ROUTE_UNFUSED 8          /* one kernel per op */
+int fh_last_route(fh_session* s, int32_t* route);
+
 /* Sampler.ApplyRepetitionControls + Sampler.Sample on one logit row already on
  * the device: logits_dev [V] (not modified), history [n_hist] host ids, u01 the
  * NextDouble for this draw.  Returns the id in *out_id. */

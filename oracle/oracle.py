@@ -128,6 +128,54 @@ def init_weights(cfg: Config, seed: int) -> np.ndarray:
     return w
 
 
+def param_layout(cfg: Config) -> list:
+    """[(name, offset, shape)] of the flat registry array, in GptModel's registration
+    order (GptModel.cs:53-91): tok_emb [V,d], pos_emb [ctx,d], per block ln1.{w,b},
+    attn.qkv.{w [d,3d], b}, attn.proj.{w [d,d], b}, ln2.{w,b}, mlp.fc.{w [d,4d], b},
+    mlp.proj.{w [4d,d], b}, then ln_f.{w,b}."""
+    V, ctx, d, L, _ = cfg.dims
+    shapes = [("tok_emb", (V, d)), ("pos_emb", (ctx, d))]
+    for i in range(L):
+        p = f"blocks.{i}."
+        shapes += [(p + "ln1.w", (d,)), (p + "ln1.b", (d,)), (p + "attn.qkv.w", (d, 3 * d)),
+                   (p + "attn.qkv.b", (3 * d,)), (p + "attn.proj.w", (d, d)), (p + "attn.proj.b", (d,)),
+                   (p + "ln2.w", (d,)), (p + "ln2.b", (d,)), (p + "mlp.fc.w", (d, 4 * d)),
+                   (p + "mlp.fc.b", (4 * d,)), (p + "mlp.proj.w", (4 * d, d)), (p + "mlp.proj.b", (d,))]
+    shapes += [("ln_f.w", (d,)), ("ln_f.b", (d,))]
+    out, off = [], 0
+    for name, shp in shapes:
+        out.append((name, off, shp))
+        off += int(np.prod(shp))
+    assert off == param_count(cfg)
+    return out
+
+
+def params(cfg: Config, weights: np.ndarray) -> dict:
+    """name -> view of `weights` with the tensor's shape."""
+    return {n: weights[o:o + int(np.prod(s))].reshape(s) for n, o, s in param_layout(cfg)}
+
+
+def trained_like(cfg: Config, weights: np.ndarray, seed: int, ln_w_std: float = 0.1, ln_b_std: float = 0.05,
+                 bias_std: float = 0.05) -> np.ndarray:
+    """A copy of `weights` whose LayerNorm and Linear vectors are no longer the
+    initial (1, 0) and 0 (GptModel.cs:65-66, 90-91): every LayerNorm weight becomes
+    1 + N(0, ln_w_std), every LayerNorm bias N(0, ln_b_std) and every Linear bias
+    N(0, bias_std), drawn from numpy's seeded generator.  Matrices are kept.  With
+    these values the LayerNorm affine (CpuBackend.cs:396) and AddBias
+    (Layers.cs:35) change every output, as they do in a trained checkpoint."""
+    out = np.array(weights, np.float32, copy=True)
+    rng = np.random.default_rng(seed)
+    for name, off, shp in param_layout(cfg):
+        n = int(np.prod(shp))
+        if name.endswith(("ln1.w", "ln2.w", "ln_f.w")):
+            out[off:off + n] = (1.0 + ln_w_std * rng.standard_normal(n)).astype(np.float32)
+        elif name.endswith(("ln1.b", "ln2.b", "ln_f.b")):
+            out[off:off + n] = (ln_b_std * rng.standard_normal(n)).astype(np.float32)
+        elif name.endswith(".b"):
+            out[off:off + n] = (bias_std * rng.standard_normal(n)).astype(np.float32)
+    return out
+
+
 def matmul_nn(a, b):
     a = np.ascontiguousarray(a, np.float32); b = np.ascontiguousarray(b, np.float32)
     y = np.empty((a.shape[0], b.shape[1]), np.float32)

@@ -175,7 +175,8 @@ def test_checkpoint_loads_into_a_session(fhp, oracle, tmp_path, dtype):
     # within the fp32 / bf16 bars
     shape = (2256, 128, 128, 4, 4)
     ocfg = oracle.Config(*shape)
-    w = oracle.init_weights(ocfg, 1234)
+    # trained-like: LayerNorm and bias vectors away from their initial 1 / 0
+    w = oracle.trained_like(ocfg, oracle.init_weights(ocfg, 1234), 77)
     be = fhp.HipBackend(0)
     cfg = fhp.ModelConfig(*shape)
     names = [n for n, _ in fhp.registry(cfg)]
@@ -202,4 +203,27 @@ def test_checkpoint_loads_into_a_session(fhp, oracle, tmp_path, dtype):
         fhp.Checkpoint.load(p, be, dtype=dtype)
     m.dispose()
     direct.dispose()
+    be.dispose()
+
+
+@pytest.mark.gpu
+def test_checkpoint_of_released_shape_decodes_on_the_fused_step(fhp, oracle, tmp_path):
+    # a FORGEMODEL1 file of the released Forge-98M configuration (V 16257, ctx 512,
+    # MODEL_CARD.md:16-17) with trained-like parameters: loaded through
+    # fh_session_load_checkpoint, which also builds the fused decode step's tiles
+    # from it, then 48 greedy ids in one fused launch equal the oracle's
+    shape = (16257, 512, 768, 12, 12)
+    ocfg = oracle.Config(*shape)
+    w = oracle.trained_like(ocfg, oracle.init_weights(ocfg, 5), 6)
+    be = fhp.HipBackend(0)
+    names = [n for n, _ in fhp.registry(fhp.ModelConfig(*shape))]
+    p = str(tmp_path / "forge98m.forge")
+    write_checkpoint(p, shape, names, w, name="Forge-98M")
+    m = fhp.Checkpoint.load(p, be)
+    prompt = fhp.TrainingRandom(42).ids(shape[0], 64)
+    ids = fhp.Sampler.generate(m, prompt, 48, 0.0, 0, None)
+    assert fhp.Sampler.last_timing["route"] == fhp._native.FH_ROUTE_FUSED_STEP
+    oracle.set_threads(8)
+    np.testing.assert_array_equal(ids, oracle.generate(ocfg, w, prompt, 48))
+    m.dispose()
     be.dispose()

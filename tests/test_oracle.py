@@ -303,3 +303,111 @@ def test_golden_net_random(oracle):
     g = np.load(os.path.join(GOLDEN, "net_random.npz"))
     for s in (0, 1, 42):
         np.testing.assert_array_equal(oracle.net_random_doubles(s, 1000), g[f"seed{s}"])
+
+
+# ---- the forward's composition (Layers.cs:384-392, GptModel.cs:212-222) ---------------------
+# The ops above are pinned one by one; these pin how the oracle composes them: block
+# order, residual placement, head layout, the causal mask and LN_f before the tied head.
+# Parameters are "trained-like" (LayerNorm affine and biases away from 1/0), so every
+# LayerNorm and bias term contributes.
+
+import gpt_f64  # noqa: E402
+
+COMP = (97, 24, 32, 3, 4)  # V, ctx, d, L, H: small enough for float64 numpy
+
+
+def _comp_weights(oracle, seed=3):
+    # qkv weights scaled up 8x: at the initial std the scores are so small that the
+    # softmax is nearly uniform, and a wrong head layout would hardly show
+    c = oracle.Config(*COMP)
+    w = oracle.trained_like(c, oracle.init_weights(c, seed), seed + 100)
+    for n, v in oracle.params(c, w).items():
+        if n.endswith("attn.qkv.w"):
+            v *= 8
+    return c, w
+
+
+def _rel(a, e):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - e) / np.maximum(1.0, np.abs(e))))
+
+
+def test_forward_single_token_closed_form(oracle):
+    # T = 1: the causal softmax over one key is exactly 1, so attention returns v
+    # itself; every block is then a closed form in x alone (no score, no softmax)
+    c, w = _comp_weights(oracle)
+    P = {n: v.astype(np.float64) for n, v in oracle.params(c, w).items()}
+    V, ctx, d, L, H = COMP
+
+    def ln(x, a, b):
+        mu = x.mean()
+        return (x - mu) / np.sqrt(((x - mu) ** 2).mean() + 1e-5) * a + b
+
+    for tok in (0, 41, 96):
+        x = P["tok_emb"][tok] + P["pos_emb"][0]
+        for i in range(L):
+            g = lambda k: P[f"blocks.{i}.{k}"]  # noqa: E731
+            v = (ln(x, g("ln1.w"), g("ln1.b")) @ g("attn.qkv.w") + g("attn.qkv.b"))[2 * d:]
+            a = v @ g("attn.proj.w") + g("attn.proj.b") + x
+            f = ln(a, g("ln2.w"), g("ln2.b")) @ g("mlp.fc.w") + g("mlp.fc.b")
+            x = 0.5 * f * (1 + np.tanh(np.sqrt(2 / np.pi) * (f + 0.044715 * f ** 3))) @ g("mlp.proj.w") \
+                + g("mlp.proj.b") + a
+        want = ln(x, P["ln_f.w"], P["ln_f.b"]) @ P["tok_emb"].T
+        assert _rel(oracle.forward(c, w, [tok])[0], want) <= 1e-5
+
+
+def test_forward_with_zero_blocks_is_ln_f_of_embeddings(oracle):
+    # every block matrix and bias zero: v = 0 so attention adds 0, fc = 0 so GELU(0) = 0
+    # and the MLP adds 0; each row's logits are LN_f(tok + pos) tok_emb^T, exactly
+    # the embedding path and the tied head
+    c, w = _comp_weights(oracle)
+    P = oracle.params(c, w)
+    for n, v in P.items():
+        if n.startswith("blocks.") and not n.endswith(("ln1.w", "ln1.b", "ln2.w", "ln2.b")):
+            v[...] = 0
+    ids = [5, 17, 5, 90, 0, 33, 62]
+    x = P["tok_emb"][ids].astype(np.float64) + P["pos_emb"][:len(ids)]
+    mu = x.mean(1, keepdims=True)
+    xn = (x - mu) / np.sqrt(((x - mu) ** 2).mean(1, keepdims=True) + 1e-5) * P["ln_f.w"] + P["ln_f.b"]
+    assert _rel(oracle.forward(c, w, ids), xn @ P["tok_emb"].T.astype(np.float64)) <= 1e-5
+
+
+@pytest.mark.parametrize("which", ["attn.proj.b", "mlp.proj.b"])
+def test_forward_with_only_output_biases_adds_them(oracle, which):
+    # only the output bias of one sub-block non-zero: each block adds exactly that bias
+    # to the residual stream (attention of v = 0 and an MLP of fc = 0 contribute
+    # nothing else), so the final x is tok + pos + sum over blocks of the bias
+    c, w = _comp_weights(oracle)
+    P = oracle.params(c, w)
+    total = np.zeros(COMP[2])
+    for n, v in P.items():
+        if n.startswith("blocks.") and not n.endswith(("ln1.w", "ln1.b", "ln2.w", "ln2.b", which)):
+            v[...] = 0
+        if n.endswith(which):
+            total += v
+    ids = [7, 3, 3, 80]
+    x = P["tok_emb"][ids].astype(np.float64) + P["pos_emb"][:len(ids)] + total
+    mu = x.mean(1, keepdims=True)
+    xn = (x - mu) / np.sqrt(((x - mu) ** 2).mean(1, keepdims=True) + 1e-5) * P["ln_f.w"] + P["ln_f.b"]
+    assert _rel(oracle.forward(c, w, ids), xn @ P["tok_emb"].T.astype(np.float64)) <= 1e-5
+
+
+def test_forward_matches_float64_restatement(oracle):
+    # the whole window (every row, causal attention over 4 heads, 3 blocks) against an
+    # independent float64 statement of the reference forward
+    c, w = _comp_weights(oracle)
+    ids = oracle.pcg32_ids(9, COMP[0], COMP[1])
+    want = gpt_f64.forward(oracle.param_layout(c), w, COMP[4], ids)
+    assert _rel(oracle.forward(c, w, ids), want) <= 1e-5
+
+
+@pytest.mark.parametrize("mutation", gpt_f64.MUTATIONS)
+def test_composition_checks_catch_mutations(oracle, mutation):
+    # each plausible composition mistake (post-LN blocks, a dropped residual, no causal
+    # mask, no LN_f, K and V swapped, heads taken as interleaved columns, LN1's
+    # parameters reused for LN2) moves the logits far outside the 1e-5 bar the oracle
+    # meets above, so the comparison would catch it in the oracle
+    c, w = _comp_weights(oracle)
+    ids = oracle.pcg32_ids(9, COMP[0], COMP[1])
+    good = gpt_f64.forward(oracle.param_layout(c), w, COMP[4], ids)
+    bad = gpt_f64.forward(oracle.param_layout(c), w, COMP[4], ids, mutate=mutation)
+    assert _rel(bad, good) > 1e-3, mutation
