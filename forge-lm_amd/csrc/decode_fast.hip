@@ -43,6 +43,7 @@
 #include <math.h>
 #include <stdlib.h>
 
+#include <algorithm>
 #include <mutex>
 #include <tuple>
 #include <vector>
@@ -65,6 +66,9 @@ constexpr int TAGS = 128;          // tag values reserved per launch
 constexpr int PH = 8;              // tagged phases per layer
 constexpr long SPIN_LIMIT = 400000;
 constexpr int PART = 68;           // pairs per attention partial: o[64], m, l, pad[2]
+
+// vocabulary rows per block of the tied head: ceil(V / 256), at least one per data wave
+__host__ __device__ __forceinline__ int head_rows(int V) { return max(NDW, (V + NB - 1) / NB); }
 
 __device__ __forceinline__ bool err_set(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
@@ -175,7 +179,7 @@ struct KParams {
   const float* tiles;
   const float* vecs;  // ln_f weight, bias
   const float* btab;
-  const float* tok;
+  const float* tok;   // tok_emb, or its copy zero-padded to 256 * R rows (the head reads whole shares)
   const float* pos;
   float* kc;
   float* vc;
@@ -191,7 +195,7 @@ struct KParams {
   unsigned* launch;   // launch counter
   int* err;
   int V, ctx, L, max_new, eos, greedy;
-  int R;              // vocabulary rows per block of the head: ceil(V / 256), rows >= V are skipped
+  int Vp;             // 256 * rows per block of the head (V rounded up, at least 768): rows >= V are skipped
   int nsteps;         // decode steps of this launch (greedy: the argmax feeds the next step)
   int* tokens_out;    // same buffer as src.tokens, written by the greedy argmax
   int* step_out;      // same word as src.step
@@ -615,7 +619,6 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
     if (l > 0 && !dead && !gather<D>(ncl, r.xl0 + XL::X, tb - PH + 7, sh.xres, p.err, err_code(W_X, l), D, &np[0]))
       fail();
     __syncthreads();
-    if (it == 0 && sh.fail) dead = true;  // a check at the kernel's start failed
     TM(0);
     if (it == r.trace_it + 1) trace_mark(p.trace, 9);
     // Every phase whose data waves publish and then request tiles has a
@@ -737,7 +740,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       const unsigned tH = tbase + PH * p.L;
       if (!dead) {
         // this block's logits (for a host-side sampler) and its argmax record
-        const int R = p.R;
+        const int R = p.Vp / NB;
         float best = -INFINITY;
         int bi = 0x7fffffff;
         if (lane < R && r.blk * R + lane < p.V) {
@@ -1161,24 +1164,21 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
     site(std::integral_constant<int, S_EEND>());
     if (run && l == p.L - 1) {
       // ---- head of token t: LN_f + tied projection over this block's vocab rows ----
-      // block b owns rows [b*R, b*R + R) below V (the last blocks hold fewer, or
-      // none, when V is not a multiple of 256); data wave w takes rows w, w+3, ...
-      const int R = p.R;
+      // block b owns rows [b*R, b*R + R) of the head table (tok_emb, zero-padded to
+      // 256 * R rows when V is not a multiple of 256; rows >= V are left out of the
+      // argmax); R >= 3, so every data wave has rows: w, w+3, ...
+      const int R = p.Vp / NB;
       constexpr int HG = FH_HG;  // rows per wave in flight
-      const int row0 = r.blk * R;
-      const int nrow = (max(0, min(R, p.V - row0)) - w + NDW - 1) / NDW;  // may be <= 0
-      // row u of this wave, clamped into the table (a wave without rows re-reads a
-      // valid row and computes nothing)
-      auto head_row = [&](int u) {
-        return p.tok + (size_t)min(max(row0 + w + NDW * min(u, nrow - 1), 0), p.V - 1) * D;
-      };
+      const float* E = p.tok + (size_t)r.blk * R * D;
+      const int nrow = (R - w + NDW - 1) / NDW;
       // the first rows are requested before the final x arrives
       float4 rh[HG * KC];
 #pragma unroll
       for (int u = 0; u < HG; u++) {
-        const float* e = head_row(u);
+        const int row = w + NDW * min(u, nrow - 1);
 #pragma unroll
-        for (int c = 0; c < KC; c++) rh[u * KC + c] = *reinterpret_cast<const float4*>(e + c * 256 + lane * 4);
+        for (int c = 0; c < KC; c++)
+          rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
       }
       __syncthreads();  // the final x is in xres
       dead = sh.fail != 0;
@@ -1197,9 +1197,10 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
           float4 nx[HG * KC];
 #pragma unroll
           for (int u = 0; u < HG; u++) {
-            const float* e = head_row(g + HG + u);
+            const int row = w + NDW * min(g + HG + u, nrow - 1);
 #pragma unroll
-            for (int c = 0; c < KC; c++) nx[u * KC + c] = *reinterpret_cast<const float4*>(e + c * 256 + lane * 4);
+            for (int c = 0; c < KC; c++)
+              nx[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
           }
 #pragma unroll
           for (int u = 0; u < HG; u++) {
@@ -1455,9 +1456,9 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   ctx = d.context_length;
   C = KPB;
   blocks = NB;
-  // the head gives each block ceil(V / 256) <= 64 vocabulary rows
+  // the head gives each block max(3, ceil(V / 256)) <= 64 vocabulary rows
   const bool shape_ok = d.dtype == FH_DTYPE_F32 && d.max_batch == 1 && D == kD && H == kH &&
-                        (V + NB - 1) / NB <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH &&
+                        head_rows(V) <= S768::RMAX && (ctx + KPB - 1) / KPB <= S768::SPH &&
                         compute_units >= NB &&
                         PH * L + 1 <= TAGS;
   if (!shape_ok) return FH_OK;
@@ -1483,6 +1484,12 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   if (hipMalloc(&tiles, tile_floats * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
   if (hipMalloc(&vecs, 2 * (size_t)D * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
   if (hipMalloc(&btab, (size_t)L * NB * S768::BT * sizeof(float)) != hipSuccess) return FH_ERR_OOM;
+  if (head_rows(V) * NB != V) {
+    // every block reads whole rows of its share: the rows past V are zeros
+    const size_t bytes = (size_t)NB * head_rows(V) * D * sizeof(float);
+    if (hipMalloc(&head, bytes) != hipSuccess) return FH_ERR_OOM;
+    if (hipMemset(head, 0, bytes) != hipSuccess) return FH_ERR_HIP;
+  }
   xch_bytes = uc_total_bytes(D);
   uc = static_cast<char*>(uc_take(device, xch_bytes));
   if (!uc) return FH_ERR_OOM;
@@ -1565,6 +1572,9 @@ int FastDecode::build(hipStream_t st, const float* const* params) {
   }
   const float* const* PF = params + 2 + 12 * L;
   if (rc == FH_OK && (!copy(PF[0], vecs, D) || !copy(PF[1], vecs + D, D))) rc = FH_ERR_HIP;
+  if (rc == FH_OK && head && hipMemcpyAsync(head, params[0], (size_t)V * D * sizeof(float), hipMemcpyDeviceToDevice,
+                                            st) != hipSuccess)
+    rc = FH_ERR_HIP;
   if (hipStreamSynchronize(st) != hipSuccess) rc = FH_ERR_HIP;
   (void)hipFree(dmap);
   return rc;
@@ -1580,7 +1590,6 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.tiles = tiles;
   k.vecs = vecs;
   k.btab = btab;
-  k.tok = s.tok_emb;
   k.pos = s.pos_emb;
   k.kc = s.kcache;
   k.vc = s.vcache;
@@ -1596,7 +1605,8 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.launch = reinterpret_cast<unsigned*>(ctl);
   k.err = reinterpret_cast<int*>(ctl) + 16;
   k.V = V;
-  k.R = (V + NB - 1) / NB;
+  k.tok = head ? head : s.tok_emb;
+  k.Vp = NB * head_rows(V);
   k.ctx = ctx;
   k.L = L;
   k.max_new = s.max_new;
@@ -1653,11 +1663,12 @@ void FastDecode::release() {
   if (tiles) (void)hipFree(tiles);
   if (vecs) (void)hipFree(vecs);
   if (btab) (void)hipFree(btab);
+  if (head) (void)hipFree(head);
   if (xl) (void)hipFree(xl);
   uc_give(device, xch_bytes, uc);
   if (ctl) (void)hipFree(ctl);
   if (trace) (void)hipFree(trace);
-  tiles = vecs = btab = nullptr;
+  tiles = vecs = btab = head = nullptr;
   xl = nullptr;
   uc = nullptr;
   ctl = nullptr;

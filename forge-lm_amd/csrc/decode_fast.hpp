@@ -19,6 +19,7 @@ struct FastDecode {
   float* tiles = nullptr;            // per-block weight tiles, column-major
   float* vecs = nullptr;             // ln_f weight and bias (LN1 / LN2 are folded into the tiles)
   float* btab = nullptr;             // per-layer, per-block bias slices
+  float* head = nullptr;             // copy of tok_emb zero-padded to a whole number of rows per block, when V needs it
   char* uc = nullptr;                // uncached hand-off area (cross-XCD pairs, argmax records)
   size_t xch_bytes = 0;
   void* xl = nullptr;                // per-XCD hand-off area (q/k/v, attention partials)

@@ -222,7 +222,8 @@ def test_sampler_exact_on_same_logits(fhp, oracle, backend):
     rng = np.random.default_rng(11)
     cases = 0
     for trial in range(60):
-        V = int(rng.choice([7, 100, 2256, 16384]))
+        # V > 16384 takes the block-per-row sampler kernel instead of the register-resident one
+        V = int(rng.choice([7, 100, 2256, 16384, 30000, 65536]))
         lg = (rng.standard_normal(V) * 2).astype(np.float32)
         if trial % 3 == 0:
             lg = np.round(lg, 1).astype(np.float32)  # ties
