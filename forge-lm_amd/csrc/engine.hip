@@ -24,6 +24,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -781,6 +782,8 @@ int fh_random_doubles(int32_t seed, int n, double* out) {
   return FH_OK;
 }
 
+static int scratch_init(int device);
+
 int fh_context_create(int device, fh_context** out) {
   if (!out) return set_err(FH_ERR_INVALID, "out is null");
   *out = nullptr;
@@ -791,6 +794,7 @@ int fh_context_create(int device, fh_context** out) {
   c->device = device;
   HIP_TRY(hipSetDevice(device));
   HIP_TRY(hipGetDeviceProperties(&c->props, device));
+  FH_TRY(scratch_init(device));  // the no-allocation sampler's scratch address on this device
   HIP_TRY(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
   *out = c.release();
   return FH_OK;
@@ -1479,45 +1483,27 @@ int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t
   return FH_OK;
 }
 
-int fh_sample_logits(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
-                     const fh_sampling* opts, double u01, int32_t* out_id) {
-  if (!c || !logits_dev || !opts || !out_id || (n_hist > 0 && !history))
-    return set_err(FH_ERR_INVALID, "null argument");
-  if (V <= 0 || V > 65536) return set_err(FH_ERR_UNSUPPORTED, "V must be in [1, 65536]");
-  if (n_hist < 0) return set_err(FH_ERR_INVALID, "n_hist must be >= 0");
-  if (!std::isfinite(opts->temperature)) return set_err(FH_ERR_INVALID, "Temperature must be finite.");
-  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty < 1.f)
-    return set_err(FH_ERR_RANGE, "Repetition penalty must be finite and >= 1.");
-  if (opts->no_repeat_ngram < 0) return set_err(FH_ERR_RANGE, "No-repeat n-gram size must be >= 0.");
-  HIP_TRY(hipSetDevice(c->device));
+// Sampler.ApplyRepetitionControls + Sampler.Sample of one device logit row with the
+// caller's scratch: work [V] floats, ints [n_hist + 5] (history, step, done, out,
+// count), u [1].  Synchronous; the id comes back through *out_id.
+static int sample_row(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                      const fh_sampling* opts, double u01, int32_t* out_id, float* work, int* ints, double* u) {
   hipStream_t st = c->stream;
-  if (V > c->s_V) {
-    dev_free(c->s_work);
-    FH_TRY(dev_alloc(&c->s_work, V));
-    c->s_V = V;
-  }
-  const int need = n_hist + 1 + 4;
-  if (need > c->s_hist) {
-    dev_free(c->s_ints);
-    FH_TRY(dev_alloc(&c->s_ints, need));
-    c->s_hist = need;
-  }
-  if (!c->s_u) FH_TRY(dev_alloc(&c->s_u, 1));
-  int* tokens = c->s_ints;
-  int* misc = c->s_ints + n_hist + 1;  // step, done, out, count
+  int* tokens = ints;
+  int* misc = ints + n_hist + 1;  // step, done, out, count: cleared for every call
   if (n_hist > 0) HIP_TRY(hipMemcpyAsync(tokens, history, sizeof(int32_t) * n_hist, hipMemcpyHostToDevice, st));
-  HIP_TRY(hipMemcpyAsync(c->s_u, &u01, sizeof(double), hipMemcpyHostToDevice, st));
+  HIP_TRY(hipMemcpyAsync(u, &u01, sizeof(double), hipMemcpyHostToDevice, st));
   const int init[4] = {0, 0, 0, -1};
   HIP_TRY(hipMemcpyAsync(misc, init, sizeof init, hipMemcpyHostToDevice, st));
   SampleArgs a{};
   a.logits = logits_dev;
-  a.work = c->s_work;
+  a.work = work;
   a.tokens = tokens;
   a.step = misc;
   a.done = misc + 1;
   a.out_ids = misc + 2;
   a.out_counts = misc + 3;
-  a.uniforms = c->s_u;
+  a.uniforms = u;
   a.dump = nullptr;
   a.B = 1;
   a.V = V;
@@ -1542,6 +1528,88 @@ int fh_sample_logits(fh_context* c, const float* logits_dev, int V, const int32_
   HIP_TRY(hipStreamSynchronize(st));
   *out_id = r;
   return FH_OK;
+}
+
+static int check_sample_args(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                             const fh_sampling* opts, int32_t* out_id) {
+  if (!c || !logits_dev || !opts || !out_id || (n_hist > 0 && !history))
+    return set_err(FH_ERR_INVALID, "null argument");
+  if (V <= 0 || V > 65536) return set_err(FH_ERR_UNSUPPORTED, "V must be in [1, 65536]");
+  if (n_hist < 0) return set_err(FH_ERR_INVALID, "n_hist must be >= 0");
+  if (!std::isfinite(opts->temperature)) return set_err(FH_ERR_INVALID, "Temperature must be finite.");
+  if (!std::isfinite(opts->repetition_penalty) || opts->repetition_penalty < 1.f)
+    return set_err(FH_ERR_RANGE, "Repetition penalty must be finite and >= 1.");
+  if (opts->no_repeat_ngram < 0) return set_err(FH_ERR_RANGE, "No-repeat n-gram size must be >= 0.");
+  return FH_OK;
+}
+
+int fh_sample_logits(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                     const fh_sampling* opts, double u01, int32_t* out_id) {
+  FH_TRY(check_sample_args(c, logits_dev, V, history, n_hist, opts, out_id));
+  HIP_TRY(hipSetDevice(c->device));
+  if (V > c->s_V) {
+    dev_free(c->s_work);
+    FH_TRY(dev_alloc(&c->s_work, V));
+    c->s_V = V;
+  }
+  const int need = n_hist + 1 + 4;
+  if (need > c->s_hist) {
+    dev_free(c->s_ints);
+    FH_TRY(dev_alloc(&c->s_ints, need));
+    c->s_hist = need;
+  }
+  if (!c->s_u) FH_TRY(dev_alloc(&c->s_u, 1));
+  return sample_row(c, logits_dev, V, history, n_hist, opts, u01, out_id, c->s_work, c->s_ints, c->s_u);
+}
+
+// ---------------------------------------------------------------------------
+// fh_sample_logits_noalloc: the same draw on a fixed scratch array in device
+// memory, for callers that must not allocate.  Layout of `scratch`: the work row
+// (FH_NOALLOC_MAX_VOCAB floats), then the uniform (one double), then the ints
+// (history of up to FH_NOALLOC_MAX_HISTORY ids, step, done, out, count).  Each
+// device holds its own copy until the process ends; host code reaches it only
+// through the per-device address from hipGetSymbolAddress (g_scratch_dev).
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchWork = (size_t)FH_NOALLOC_MAX_VOCAB * sizeof(float);
+constexpr size_t kScratchU = kScratchWork;
+constexpr size_t kScratchInts = kScratchU + 256;
+constexpr size_t kScratchBytes = kScratchInts + ((size_t)FH_NOALLOC_MAX_HISTORY + 5) * sizeof(int);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::vector<unsigned char*> g_scratch_dev;  // per device id: the device address of `scratch`
+
+// Resolves `scratch`'s address on the current device (once per device); called by
+// fh_context_create with the context's device current.
+static int scratch_init(int device) {
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if ((size_t)device < g_scratch_dev.size() && g_scratch_dev[device]) return FH_OK;
+  void* ptr = nullptr;
+  hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !ptr)
+    return set_err(FH_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+  if ((size_t)device >= g_scratch_dev.size()) g_scratch_dev.resize(device + 1, nullptr);
+  g_scratch_dev[device] = static_cast<unsigned char*>(ptr);
+  return FH_OK;
+}
+
+int fh_sample_logits_noalloc(fh_context* c, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                             const fh_sampling* opts, double u01, int32_t* out_id) {
+  FH_TRY(check_sample_args(c, logits_dev, V, history, n_hist, opts, out_id));
+  if (V > FH_NOALLOC_MAX_VOCAB)
+    return set_err(FH_ERR_RANGE, "V (%d) exceeds the no-allocation scratch (%d)", V, FH_NOALLOC_MAX_VOCAB);
+  if (n_hist > FH_NOALLOC_MAX_HISTORY)
+    return set_err(FH_ERR_RANGE, "history of %d ids exceeds the no-allocation scratch (%d)", n_hist,
+                   FH_NOALLOC_MAX_HISTORY);
+  unsigned char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if ((size_t)c->device < g_scratch_dev.size()) base = g_scratch_dev[c->device];
+  }
+  if (!base) return set_err(FH_ERR_STATE, "no scratch address for device %d", c->device);
+  HIP_TRY(hipSetDevice(c->device));
+  return sample_row(c, logits_dev, V, history, n_hist, opts, u01, out_id, reinterpret_cast<float*>(base),
+                    reinterpret_cast<int*>(base + kScratchInts), reinterpret_cast<double*>(base + kScratchU));
 }
 
 }  // extern "C"

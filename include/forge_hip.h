@@ -198,6 +198,20 @@ int fh_last_route(fh_session* s, int32_t* route);
 int fh_sample_logits(fh_context* ctx, const float* logits_dev, int V, const int32_t* history,
                      int n_hist, const fh_sampling* opts, double u01, int32_t* out_id);
 
+/* fh_sample_logits without any device allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory (tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, checks and result as fh_sample_logits, but
+ * the scratch (the work row, the uploaded history, the uniform and the result) is
+ * one fixed array in device memory that each device holds until the process ends
+ * (about 392 KB), so V may be at most FH_NOALLOC_MAX_VOCAB and n_hist at most
+ * FH_NOALLOC_MAX_HISTORY (FH_ERR_RANGE otherwise).  Every call on one device shares
+ * that array: calls that overlap on one device (from several threads or contexts)
+ * race and must be serialised by the caller. */
+#define FH_NOALLOC_MAX_VOCAB 65536
+#define FH_NOALLOC_MAX_HISTORY 32768
+int fh_sample_logits_noalloc(fh_context* ctx, const float* logits_dev, int V, const int32_t* history, int n_hist,
+                             const fh_sampling* opts, double u01, int32_t* out_id);
+
 /* ---- op-level ITensorBackend on device buffers ---------------------------------
  * One entry point per ITensorBackend method (src/LLM.Core/Tensor/ITensorBackend.cs);
  * every tensor argument is a device pointer to row-major fp32 of the documented
