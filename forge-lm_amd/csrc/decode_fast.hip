@@ -40,6 +40,7 @@
 // HBM streams continuously while the control wave waits.  Cached K/V rows are
 // requested before x arrives.  Every wait is bounded: past the spin limit the
 // error word is set and all blocks leave.
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 
@@ -70,6 +71,11 @@ constexpr int PART = 68;           // pairs per attention partial: o[64], m, l, 
 // vocabulary rows per block of the tied head: ceil(V / 256), at least one per data wave
 __host__ __device__ __forceinline__ int head_rows(int V) { return max(NDW, (V + NB - 1) / NB); }
 
+// The sampled kernel keeps the window's ids in LDS (ctx <= 1536) and draws with
+// top-k <= KMAX inside the launch.
+constexpr int HCAP = 1536;
+constexpr int KMAX = 63;
+
 __device__ __forceinline__ bool err_set(int* err) {
   return __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
 }
@@ -77,9 +83,12 @@ __device__ __forceinline__ bool err_set(int* err) {
 // (waits: 1 x, 2 q/k/v, 3 attention partials, 5 attn.proj partials, 6 x2, 7 h,
 // 8 mlp.proj partials, 9 final x, 10 argmax; 4 is not used), or which check
 // failed (11 a token id outside [0, V), 12 two blocks of the launch on the same
-// (XCD, slot)).  A wait that gives up because another block already failed
-// records nothing.
-enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX, W_TOK, W_XCD };
+// (XCD, slot), 13 the in-kernel sampler met a non-finite logit or an exact tie at
+// a top-k threshold: the host then repeats the generation on the per-step path;
+// 14 and 15 the sampler's two waits).  A wait that gives up because another block
+// already failed records nothing.
+enum WaitId { W_X = 1, W_QKV, W_PART, W_O, W_PX2, W_X2, W_H, W_PX, W_XF, W_AMAX, W_TOK, W_XCD, W_SAMPLE, W_SKEYS,
+              W_SLIST };
 __device__ __forceinline__ int err_code(int wait, int l) {
   return (int)(0x80000000u | ((unsigned)wait << 24) | ((unsigned)(l & 0xff) << 16) | blockIdx.x);
 }
@@ -171,7 +180,8 @@ struct Xl {
   static constexpr int X2 = PARTS + S::HPX * S::SPH * PART;       // x2 (every XCD keeps a copy)
   static constexpr int HH = X2 + D;                               // the XCD's h slice
   static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
-  static constexpr int STRIDE = X + D;
+  static constexpr int SAMP = X + D;                              // sampler keys: 64 per block of the XCD
+  static constexpr int STRIDE = SAMP + SLOTS * 64;
 };
 
 struct KParams {
@@ -190,12 +200,17 @@ struct KParams {
   int uc_bytes;
   int off_amax;       // byte offset of the argmax records in uc
   int off_claim;      // byte offset of the (XCD, slot) claim words in uc
+  int off_slist;      // byte offset of the sampler's per-XCD top-k lists in uc (8 x 64 records)
   uint2* xl;          // per-XCD pairs (Xl), ordinary device memory
   int xl_bytes;
   unsigned* launch;   // launch counter
   int* err;
   int V, ctx, L, max_new, eos, greedy;
   int Vp;             // 256 * rows per block of the head (V rounded up, at least 768): rows >= V are skipped
+  // sampled kernel: Sampler.Sample with top-k after ApplyRepetitionControls (Sampler.cs:29-69, 111-165)
+  const double* uniforms;  // [max_new]: the NextDouble of step n
+  float temperature, penalty;
+  int top_k, ngram;
   int nsteps;         // decode steps of this launch (greedy: the argmax feeds the next step)
   int* tokens_out;    // same buffer as src.tokens, written by the greedy argmax
   int* step_out;      // same word as src.step
@@ -535,12 +550,30 @@ struct Lds {
   int fail;
 };
 
+// LDS of the sampled kernel's sampler: the window's ids, the XCD leader's 2048
+// gathered values, and the selection scratch
+template <bool SAMPLED>
+struct SampLds {
+  int hist[1];
+  float g[1];
+  float cv[1];
+  int cr[1];
+};
+template <>
+struct SampLds<true> {
+  int hist[HCAP];
+  float g[64];
+  float cv[NB / NX * 64];
+  int cr[NB / NX * 64];
+};
+
 // What this block and wave do in the step
 struct Role {
   int blk, w, lane, xcd, slot, vb;
   int nh, qc, qcw;      // heads of the XCD; qkv columns of the block and of a data wave
   int hj, kb, ah;       // attention: local head, key block, global head
   int n0, pos0;         // first step of the launch and its position
+  int nh0;              // ids in the window before the launch's first step (sampled kernel)
   int pos, nk;          // the current token's position and key count
   int nkb;              // key blocks per head (attention blocks) for every token of the launch
   int key0;             // this data wave's first key
@@ -589,8 +622,300 @@ __device__ bool gather_argmax(const B& nc, int off, unsigned tag, float& best, i
   return true;
 }
 
+// ---- the sampled kernel's sampler (one wave) ----------------------------------------
+// Sampler.Sample with top-k (Sampler.cs:29-69) after ApplyRepetitionControls
+// (:111-165), spread over the launch's blocks: each block adjusts its own rows,
+// each XCD's first block selects the XCD's k largest, and every block selects the
+// k largest of the 8 XCD lists and draws.  The arithmetic is the reference's, in its
+// order: penalty (x < 0 ? x * p : x / p), division by T, the threshold = the k-th
+// largest value with ties kept, exp(p - max) summed in index order, u = (float)U * sum,
+// the first index whose running sum exceeds u.
+
+__device__ __forceinline__ float wave_fmax(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_fmin(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_or64(uint64_t v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    lo |= (uint32_t)__shfl_xor((int)lo, o, 64);
+    hi |= (uint32_t)__shfl_xor((int)hi, o, 64);
+  }
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// The k-th largest (duplicates counted) of the values v[j] of every lane (absent
+// entries are -inf and are never counted; at least k are present), and, in cv/cr
+// (LDS, cap entries), the entries >= that value with their rows, *n of them.
+// A window [lo, M] below the maximum M that holds at least k values is narrowed:
+// first the steps M - 2^q / 8 (q < 8), then 8 halvings between the last step that
+// held fewer than k and the first that held k (counts by ballot), so it keeps
+// little more than k candidates; the k-th largest is the smallest candidate with
+// fewer than k candidates above it.
+template <int N>
+__device__ float wave_topk(const float (&v)[N], const int (&row)[N], int k, float* cv, int* cr, int cap, int* n) {
+  const int lane = threadIdx.x & 63;
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < N; j++) m = fmaxf(m, v[j]);
+  const float M = wave_fmax(m);
+  auto count_ge = [&](float b) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < N; j++) c += __popcll(__ballot(v[j] >= b));
+    return c;
+  };
+  float lo = M;
+  if (count_ge(M) < k) {
+    float hi = M;
+    lo = -FLT_MAX;
+    for (int q = 0; q < 8; q++) {
+      const float b = M - (float)(1 << q) * 0.125f;
+      if (count_ge(b) >= k) {
+        lo = b;
+        break;
+      }
+      hi = b;
+    }
+    if (lo != -FLT_MAX) {
+      for (int h = 0; h < 8; h++) {
+        const float mid = lo + (hi - lo) * 0.5f;
+        if (count_ge(mid) >= k)
+          lo = mid;
+        else
+          hi = mid;
+      }
+    }
+  }
+  // the window's entries into LDS (order of lanes, then registers)
+  int w = 0;
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    const bool in = v[j] >= lo;
+    const uint64_t bal = __ballot(in);
+    const int pos = w + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+    if (in && pos < cap) {
+      cv[pos] = v[j];
+      cr[pos] = row[j];
+    }
+    w += __popcll(bal);
+  }
+  w = min(w, cap);
+  wave_lds_sync();
+  // rank in the window: the threshold is the smallest entry with fewer than k above it
+  float cand = INFINITY;
+  if (w <= 64) {
+    const float e = lane < w ? cv[lane] : -INFINITY;
+    int above = 0;
+    for (int j = 0; j < w; j++) above += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j)) > e ? 1 : 0;
+    if (lane < w && above < k) cand = e;
+  } else {  // many equal or dense values near the k-th largest
+    for (int i = lane; i < w; i += 64) {
+      const float e = cv[i];
+      int above = 0;
+      for (int j = 0; j < w; j++) above += cv[j] > e ? 1 : 0;
+      if (above < k) cand = fminf(cand, e);
+    }
+  }
+  const float thr = wave_fmin(cand);
+  // keep the entries >= thr (their count is k unless values tie at thr)
+  wave_lds_sync();
+  int c = 0;
+  for (int base = 0; base < w; base += 64) {
+    const int i = base + lane;
+    const float e = i < w ? cv[i] : -INFINITY;
+    const int r = i < w ? cr[i] : 0;
+    const bool keep = e >= thr;
+    const uint64_t bal = __ballot(keep);
+    const int pos = c + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0));
+    wave_lds_sync();  // every lane has read entry i before the kept ones are moved down
+    if (keep) {
+      cv[pos] = e;
+      cr[pos] = r;
+    }
+    c += __popcll(bal);
+  }
+  wave_lds_sync();
+  *n = c;
+  return thr;
+}
+
+// ApplyRepetitionControls' masks for rows [row0, row0 + R) of one block over the
+// window's T ids hs[0..T): pm the rows the penalty scales (each distinct id once,
+// Sampler.cs:117-127), bm the rows the n-gram rule bans (:129-154).  Every lane
+// gets both masks.
+__device__ void sampler_masks(const KParams& p, const int* hs, int T, int row0, int R, uint64_t& pm, uint64_t& bm) {
+  const int lane = threadIdx.x & 63;
+  pm = 0;
+  bm = 0;
+  if (p.penalty != 1.f || p.ngram == 1) {
+    uint64_t m = 0;
+    for (int i = lane; i < T; i += 64) {
+      const int d = hs[i] - row0;
+      if ((unsigned)d < (unsigned)R) m |= 1ull << d;
+    }
+    m = wave_or64(m);
+    if (p.penalty != 1.f) pm = m;
+    if (p.ngram == 1) bm = m;
+  }
+  if (p.ngram > 1 && T >= p.ngram - 1) {
+    const int pre = p.ngram - 1, suf = T - pre;
+    uint64_t m = 0;
+    for (int s0 = lane; s0 + p.ngram <= T; s0 += 64) {
+      bool match = true;
+      for (int j = 0; j < pre; j++)
+        if (hs[s0 + j] != hs[suf + j]) {
+          match = false;
+          break;
+        }
+      const int d = hs[s0 + pre] - row0;
+      if (match && (unsigned)d < (unsigned)R) m |= 1ull << d;
+    }
+    bm = wave_or64(m);
+  }
+}
+
+// Control wave, sampled kernel, head of token t: this block's rows adjusted and
+// published; the XCD's first block selects and publishes the XCD's k largest; with
+// need_id, every block selects the k largest of the 8 XCD lists and draws the id.
+// The host only runs this kernel where no row can be all-banned and every XCD has
+// more than k unbanned rows.  Returns false after a failed wait or check (the
+// error word is set).
 template <int D, int H>
-__device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const Role& r, const bool attn) {
+__device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true>& sl, const Role& r, unsigned tH,
+                             uint64_t pm, uint64_t bm, bool need_id, double u01, int& id) {
+#pragma clang fp contract(off)
+  using XL = Xl<D, H>;
+  const int lane = threadIdx.x & 63;
+  const int R = p.Vp / NB, K = p.top_k;
+  const int row = r.vb * R + lane;
+  const bool valid = lane < R && row < p.V;
+  float x = valid ? sh.hval[lane] : 0.f;
+  if (__any(valid && !(fabsf(x) <= FLT_MAX))) {  // a NaN or infinite logit: the per-step sampler handles it
+    if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
+    return false;
+  }
+  if ((pm >> lane) & 1ull) x = x < 0.f ? x * p.penalty : x / p.penalty;
+  const float pv = (valid && !((bm >> lane) & 1ull)) ? x / p.temperature : -INFINITY;  // banned: -inf
+  const unsigned tS1 = tH + 1, tS2 = tH + 2;
+  put_pair(r.xl + XL::SAMP + r.slot * 64 + lane, pv, tS1);
+  char* ucb = reinterpret_cast<char*>(p.uc);
+  if (r.slot == 0) {
+    // the XCD's k largest of its 32 x 64 values: pair q of the XCD's area is slot
+    // q / 64, lane q % 64, i.e. row (8 (q / 64) + xcd) R + q % 64; this lane's
+    // 16-byte loads hold pairs 128 i + 2 lane and + 1
+    const LcBuf ncl(p.xl, p.xl_bytes);
+    float v[SLOTS];
+    int rw[SLOTS];
+    {
+      long it = 0;
+      for (;;) {
+        reload_fence();
+        uint4 a[SLOTS / 2];
+#pragma unroll
+        for (int i = 0; i < SLOTS / 2; i++) a[i] = ncl.load4((r.xl0 + XL::SAMP + 128 * i + 2 * lane) * 8);
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < SLOTS / 2; i++) {
+          ok &= (a[i].y == tS1) & (a[i].w == tS1);
+          v[2 * i] = __uint_as_float(a[i].x);
+          v[2 * i + 1] = __uint_as_float(a[i].z);
+        }
+        if (__all(ok)) break;
+        if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+          if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SKEYS, 0));
+          return false;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < SLOTS / 2; i++)
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const int q = 128 * i + 2 * lane + e;
+          rw[2 * i + e] = ((q >> 6) * NX + r.xcd) * R + (q & 63);
+        }
+    }
+    int cnt = 0;
+    wave_topk<SLOTS>(v, rw, K, sl.cv, sl.cr, SLOTS * 64, &cnt);
+    if (cnt != K) {  // values tie at the XCD's k-th largest
+      if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
+      return false;
+    }
+    if (lane < K)
+      *reinterpret_cast<uint4*>(ucb + p.off_slist + (r.xcd * 64 + lane) * 16) =
+          make_uint4(__float_as_uint(sl.cv[lane]), (unsigned)sl.cr[lane], tS2, tS2);
+  }
+  if (!need_id) return true;
+  // the k largest of the 8 XCD lists (record j: list j / K, entry j % K)
+  const NcBuf ncu(p.uc, p.uc_bytes);
+  float g[NX];
+  int gr[NX];
+  long it = 0;
+  for (;;) {
+    reload_fence();
+    uint4 a[NX];
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const int j = min(i * 64 + lane, NX * K - 1);
+      a[i] = ncu.load4(p.off_slist + ((j / K) * 64 + j % K) * 16);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NX; i++) {
+      const bool in = i * 64 + lane < NX * K;
+      ok &= !in || ((a[i].z == tS2) & (a[i].w == tS2));
+      g[i] = in ? __uint_as_float(a[i].x) : -INFINITY;
+      gr[i] = (int)a[i].y;
+    }
+    if (__all(ok)) break;
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SLIST, 0));
+      return false;
+    }
+  }
+  int cnt = 0;
+  wave_topk<NX>(g, gr, K, sl.cv, sl.cr, NX * 64, &cnt);
+  if (cnt != K) {  // values tie at the k-th largest: the reference keeps them all
+    if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
+    return false;
+  }
+  // the kept values, their maximum, and their order by row (Sampler.cs:52-68 walks
+  // the rows in index order: the exps summed one by one, the first row past u)
+  const float e0 = lane < K ? sl.cv[lane] : -INFINITY;
+  const int r0 = lane < K ? sl.cr[lane] : 0x7fffffff;
+  const float mx = wave_fmax(e0);
+  int rank = 0;
+  for (int j = 0; j < K; j++) rank += sl.cr[j] < r0 ? 1 : 0;
+  wave_lds_sync();
+  if (lane < K) {
+    sl.g[rank] = e0;
+    sl.cr[SLOTS * 32 + rank] = r0;
+  }
+  wave_lds_sync();
+  const float ps = lane < K ? sl.g[lane] : -INFINITY;
+  const int rs = lane < K ? sl.cr[SLOTS * 32 + lane] : 0;
+  const float ex = lane < K ? expf(ps - mx) : 0.f;
+  float acc = 0.f, pre = 0.f;
+  for (int j = 0; j < K; j++) {
+    acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j));
+    if (lane == j) pre = acc;
+  }
+  const float u = (float)u01 * acc;
+  const uint64_t hit = __ballot(lane < K && u < pre);
+  id = hit ? __builtin_amdgcn_readlane(rs, (int)__builtin_ctzll(hit)) : p.V - 1;
+  return true;
+}
+
+template <int D, int H, bool SAMPLED>
+__device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampLds<SAMPLED>& sl, const Role& r,
+                                          const bool attn) {
   using S = Shape<D, H>;
   using U = Xu<D>;
   using XL = Xl<D, H>;
@@ -736,9 +1061,42 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
       const bool thead = it == r.trace_it + p.L - 2;  // the head of the traced token
       if (thead) trace_mark(p.trace, 16);
       __syncthreads();  // x is in xres: the data waves compute this block's logits
+      uint64_t pmask = 0, bmask = 0;
+      double u01 = 0.0;
+      if constexpr (SAMPLED) {
+        u01 = p.uniforms[r.n0 + t];  // this step's NextDouble, requested before the waits
+        // ApplyRepetitionControls' penalty and n-gram bans for this block's rows
+        // (Sampler.cs:117-154) over the window's ids, while the data waves compute
+        if (!dead) sampler_masks(p, sl.hist, r.nh0 + t, r.vb * (p.Vp / NB), p.Vp / NB, pmask, bmask);
+      }
       __syncthreads();  // hval holds them
       const unsigned tH = tbase + PH * p.L;
-      if (!dead) {
+      if constexpr (SAMPLED) {
+        const bool next = t + 1 < p.nsteps;
+        int bi = 0;
+        if (!dead && !sampler_draw<D, H>(p, sh, sl, r, tH, pmask, bmask, next || r.blk == 0, u01, bi)) fail();
+        if (!dead && (next || r.blk == 0)) {
+          const int n = r.n0 + t;
+          if (r.blk == 0 && lane == 0) {
+            p.tokens_out[p.src.tok_off + 1 + n] = bi;  // window position prompt_len + n
+            if (n < p.max_new) p.out_ids[n] = bi;
+            if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+            *p.step_out = n + 1;
+          }
+          if (next) {
+            if (lane == 0) sl.hist[r.nh0 + t] = bi;  // the window grows by the drawn id
+            const float* te = p.tok + (size_t)bi * D;
+            const float* pe = p.pos + (size_t)(r.pos0 + t + 1) * D;
+#pragma unroll
+            for (int c = 0; c < S::KC; c++) {
+              const int i = c * 256 + lane * 4;
+              const float4 a = *reinterpret_cast<const float4*>(te + i);
+              const float4 b = *reinterpret_cast<const float4*>(pe + i);
+              *reinterpret_cast<float4*>(sh.xres + i) = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+            }
+          }
+        }
+      } else if (!dead) {
         // this block's logits (for a host-side sampler) and its argmax record
         const int R = p.Vp / NB;
         float best = -INFINITY;
@@ -755,6 +1113,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
           *reinterpret_cast<uint4*>(reinterpret_cast<char*>(p.uc) + p.off_amax + 16 * r.blk) =
               make_uint4(__float_as_uint(best), (unsigned)bi, tH, 0u);
       }
+      if constexpr (!SAMPLED) {
       if (thead) trace_mark(p.trace, 17);
       const bool next = t + 1 < p.nsteps;
       // Every block reduces the 256 uncached records itself (one hop; a two-level
@@ -793,6 +1152,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, const
           }
         }
       }
+      }  // greedy
       __syncthreads();  // the next token's x is in xres
       if (thead) trace_mark(p.trace, 19);
     }
@@ -849,7 +1209,7 @@ enum Site : int { S_AEND = 0, S_BSTART = 1, S_BEND = 2, S_CEND = 3, S_DEND = 4, 
 #ifndef FH_AM
 #define FH_AM S_EEND
 #endif
-template <int D, int H, bool ATTN>
+template <int D, int H, bool ATTN, bool SAMPLED>
 __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role r) {
   using S = Shape<D, H>;
   using U = Xu<D>;
@@ -1169,7 +1529,8 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       // argmax); R >= 3, so every data wave has rows: w, w+3, ...
       const int R = p.Vp / NB;
       constexpr int HG = FH_HG;  // rows per wave in flight
-      const float* E = p.tok + (size_t)r.blk * R * D;
+      // (the sampled kernel gives block vb the rows of vb: an XCD's blocks know each other's rows)
+      const float* E = p.tok + (size_t)(SAMPLED ? r.vb : r.blk) * R * D;
       const int nrow = (R - w + NDW - 1) / NDW;
       // the first rows are requested before the final x arrives
       float4 rh[HG * KC];
@@ -1225,11 +1586,12 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
 #undef DSYNC
 }
 
-template <int D, int H>
+template <int D, int H, bool SAMPLED>
 __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   using S = Shape<D, H>;
   using XL = Xl<D, H>;
   __shared__ Lds<D, H> sh;
+  __shared__ SampLds<SAMPLED> sl;
 
   Role r;
   const int tid = threadIdx.x;
@@ -1258,6 +1620,9 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   r.pos0 = p.src.pos_off + p.src.pos_mul * r.n0;  // position of the first new token (>= 1)
   r.pos = r.pos0;
   r.nk = r.pos0 + 1;
+  r.nh0 = p.src.tok_off + r.n0 + 1;  // the window: ids 0 .. prompt_len + n0 - 1
+  if constexpr (SAMPLED)
+    for (int i = tid; i < r.nh0; i += NT) sl.hist[i] = p.src.tokens[i];  // read after the loops' first barrier
   int tokid = p.src.tokens[p.src.tok_off + r.n0];
   bool bad = false;
   if ((unsigned)tokid >= (unsigned)p.V) {  // never read outside the table: report it and run no step
@@ -1303,12 +1668,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   // the block's role, that meet at the same sequence of barriers; after a
   // failed wait every wave runs on to the end without waiting or storing.
   if (ctrl) {
-    ctrl_loop<D, H>(p, sh, r, attn_blk);
+    ctrl_loop<D, H, SAMPLED>(p, sh, sl, r, attn_blk);
   } else {
     if (attn_blk)
-      data_loop<D, H, true>(p, sh, r);
+      data_loop<D, H, true, SAMPLED>(p, sh, r);
     else
-      data_loop<D, H, false>(p, sh, r);
+      data_loop<D, H, false, SAMPLED>(p, sh, r);
   }
   if (ctrl && p.trace && r.lane < 32) p.trace[r.blk * TRACE_PER + 32 + r.lane] = sh.trd[r.lane];
   trace_mark(p.trace, 31);
@@ -1399,7 +1764,8 @@ using S768 = Shape<kD, kH>;
 size_t uc_pairs_bytes(int D) { return (size_t)Xu<kD>::NPAIR * sizeof(uint2) * (D / kD); }
 size_t uc_amax_off(int D) { return (uc_pairs_bytes(D) + 255) / 256 * 256; }
 size_t uc_claim_off(int D) { return uc_amax_off(D) + (size_t)NB * sizeof(uint4); }
-size_t uc_total_bytes(int D) { return uc_claim_off(D) + (size_t)NB * sizeof(unsigned); }
+size_t uc_slist_off(int D) { return (uc_claim_off(D) + (size_t)NB * sizeof(unsigned) + 255) / 256 * 256; }
+size_t uc_total_bytes(int D) { return uc_slist_off(D) + (size_t)NX * 64 * sizeof(uint4); }
 
 // Host maps, all per virtual block vb = slot * 8 + XCD:
 //   q  qkv columns by XCD head ownership          f  mlp.fc columns: the XCD's h slice
@@ -1463,8 +1829,10 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
                         PH * L + 1 <= TAGS;
   if (!shape_ok) return FH_OK;
   int occ = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH>, NT, 0) != hipSuccess || occ < 1)
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH, false>, NT, 0) != hipSuccess || occ < 1)
     return FH_OK;
+  sampled_ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH, true>, NT, 0) == hipSuccess &&
+               occ >= 1;
   if (hipGetDevice(&device) != hipSuccess) return FH_ERR_HIP;
   {
     // the XCD-local hand-offs need 8 XCDs dealt blocks round-robin (blocks
@@ -1585,6 +1953,8 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   if (!s.src.tokens || !s.src.step || !s.tokens || !s.step || !s.kcache || !s.vcache || !s.logits || !s.out_ids ||
       !s.out_counts || s.src.pos_mul != 1 || s.max_new <= 0 || s.nsteps < 1 || (s.nsteps > 1 && !s.greedy))
     return FH_ERR_INVALID;
+  if (s.sampled && !sampler_fits(s.top_k, s.window_end))
+    return FH_ERR_INVALID;
   KParams k{};
   k.src = s.src;
   k.tiles = tiles;
@@ -1600,6 +1970,7 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.uc_bytes = (int)xch_bytes;
   k.off_amax = (int)uc_amax_off(D);
   k.off_claim = (int)uc_claim_off(D);
+  k.off_slist = (int)uc_slist_off(D);
   k.xl = reinterpret_cast<uint2*>(xl);
   k.xl_bytes = (int)xl_bytes;
   k.launch = reinterpret_cast<unsigned*>(ctl);
@@ -1616,7 +1987,15 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.tokens_out = s.tokens;
   k.step_out = s.step;
   k.trace = trace;
-  hipLaunchKernelGGL((k_decode_step<kD, kH>), dim3(NB), dim3(NT), 0, st, k);
+  k.uniforms = s.uniforms;
+  k.temperature = s.temperature;
+  k.penalty = s.penalty;
+  k.top_k = s.top_k;
+  k.ngram = s.ngram;
+  if (s.sampled)
+    hipLaunchKernelGGL((k_decode_step<kD, kH, true>), dim3(NB), dim3(NT), 0, st, k);
+  else
+    hipLaunchKernelGGL((k_decode_step<kD, kH, false>), dim3(NB), dim3(NT), 0, st, k);
   return hipGetLastError() == hipSuccess ? FH_OK : FH_ERR_HIP;
 }
 
@@ -1648,6 +2027,17 @@ int FastDecode::reset_state() {
 }
 
 int FastDecode::reset() { return enabled ? reset_state() : FH_OK; }
+
+// The sampled kernel draws inside the launch when 0 < k <= 63, the window never
+// exceeds its history buffer, and every XCD keeps more than k unbanned rows (an
+// XCD has 32 * rows-per-block rows, fewer by the padding past V, and at most
+// window_end of them are banned or penalised away): then no row set is all-banned and
+// every selection has k candidates.
+bool FastDecode::sampler_fits(int top_k, int window_end) const {
+  const int R = head_rows(V);
+  return enabled && sampled_ok && top_k > 0 && top_k <= KMAX && top_k < V && window_end <= HCAP &&
+         window_end <= ctx && SLOTS * R - (NB * R - V) - window_end > KMAX;
+}
 
 int FastDecode::check_error(unsigned* code) {
   if (code) *code = 0;

@@ -49,6 +49,13 @@ struct FastDecode {
                          // n + 1 starts from the argmax of step n, without the host
     int* tokens;         // mutable views of src.tokens / src.step
     int* step;
+    // sampled: the launch draws every step itself (Sampler.Sample with top-k after
+    // ApplyRepetitionControls) from uniforms[n]; needs sampler_fits(top_k, window_end)
+    int sampled = 0;
+    const double* uniforms = nullptr;
+    float temperature = 0.f, penalty = 1.f;
+    int top_k = 0, ngram = 0;
+    int window_end = 0;  // the window's length after the launch's last step
   };
   int enqueue(hipStream_t st, const Step& s);
   // Called before n more launches (graph replays included); resets the tag
@@ -58,6 +65,9 @@ struct FastDecode {
   // says which: 1 << 31 | wait << 24 | layer << 16 | block.
   int check_error(unsigned* code = nullptr);
   int reset();  // fresh launch counter, cleared hand-off area and error word
+  // Whether a sampled launch can run these options with windows up to window_end ids.
+  bool sampler_fits(int top_k, int window_end) const;
+  bool sampled_ok = false;  // the sampled kernel fits on the device
   void release();
 
  private:

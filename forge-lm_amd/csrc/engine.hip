@@ -55,6 +55,10 @@ using namespace fh;
 // ---------------------------------------------------------------------------
 static thread_local std::string g_err;
 
+// gen_collect's answer when a persistent sampled launch reported a case for the
+// per-step sampler (not returned across the C ABI: fh_generate repeats the generation)
+constexpr int kRetryPerStep = -100;
+
 static int set_err(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -205,6 +209,7 @@ struct GenState {
   int next = 0;         // first step not yet enqueued (step 0 is the prompt's forward)
   int n_dec = 0, n_re = 0;
   bool persistent = false, dump = false, sampled = false;
+  bool persist_sampled = false;  // the persistent launches also draw (sampled kernel)
   bool deferred = false;  // sampled, uniforms supplied per fh_generate_next call
   fh_sampling opts{};
   StepPlan plan;        // plan.opts points at opts
@@ -249,6 +254,7 @@ struct fh_session {
   bool fast_allowed = true;  // FORGE_HIP_FUSED_DECODE=0 at session creation selects the generic kernels
   bool bf16_act = true;      // FORGE_HIP_BF16_ACT=0 keeps a bf16 session's window GEMMs on fp32 operands
   bool counted = false;      // holds a reference on its context
+  bool no_sampled_fused = false;  // set while fh_generate repeats a generation on the per-step path
   bool use_fast() const { return fast.enabled && fast_allowed; }
   // generation in progress
   GenState gen;
@@ -611,7 +617,8 @@ bool fused_greedy(const fh_session* s, const fh_sampling* o) {
          s->dump == nullptr;
 }
 
-FastDecode::Step fused_step(fh_session* s, const StepPlan& p, int greedy, int nsteps) {
+FastDecode::Step fused_step(fh_session* s, const StepPlan& p, int greedy, int nsteps, bool sampled = false,
+                            int window_end = 0) {
   FastDecode::Step fs{};
   fs.src = RowSrc{s->tokens, s->step, p.tok_stride, p.P - 1, p.P - 1, 1};
   fs.tok_emb = s->v(s->idx_tok());
@@ -627,6 +634,15 @@ FastDecode::Step fused_step(fh_session* s, const StepPlan& p, int greedy, int ns
   fs.nsteps = nsteps;
   fs.tokens = s->tokens;
   fs.step = s->step;
+  if (sampled) {
+    fs.sampled = 1;
+    fs.uniforms = s->uniforms;
+    fs.temperature = p.opts->temperature;
+    fs.penalty = p.opts->repetition_penalty;
+    fs.top_k = p.opts->top_k;
+    fs.ngram = p.opts->no_repeat_ngram;
+    fs.window_end = window_end;
+  }
   return fs;
 }
 
@@ -1232,7 +1248,7 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
 // Validation (Sampler.cs:82-89, 169-175), buffers, prompt upload and the step
 // graphs of a generation; nothing is enqueued yet.  The state lives in s->gen.
 static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
-                     const double* uniforms, bool dump, bool deferred_uniforms = false) {
+                     const double* uniforms, bool dump, bool deferred_uniforms = false, bool one_shot = false) {
   s->gen.active = false;
   if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
   if (P <= 0) return set_err(FH_ERR_INVALID, "Need at least one prompt token.");
@@ -1304,6 +1320,12 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   // greedy on the fused kernel: launches run whole runs of cached steps (the
   // argmax of a step feeds the next inside the kernel); otherwise one graph per step
   g.persistent = g.n_dec > 0 && fused_greedy(s, opts);
+  // sampled with top-k (fh_generate only): the persistent launches draw in-kernel too
+  if (!g.persistent && one_shot && !s->no_sampled_fused && g.n_dec > 0 && s->use_fast() && sampled && !dump &&
+      s->fast.sampler_fits(opts->top_k, P + g.n_dec)) {
+    g.persistent = true;
+    g.persist_sampled = true;
+  }
   if (rc == FH_OK && g.n_dec > 0 && !g.persistent) {
     GraphKey k = key;
     k.kind = 0;
@@ -1317,7 +1339,8 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   s->dump = saved_dump;
   s->uniforms = saved_u;
   if (rc != FH_OK) return rc;
-  s->route = g.persistent ? FH_ROUTE_FUSED_STEP : (g.n_dec > 0 ? s->g_decode.route : 0);
+  s->route = g.persistent ? (FH_ROUTE_FUSED_STEP | (g.persist_sampled ? FH_ROUTE_FUSED_SAMPLER : 0))
+                          : (g.n_dec > 0 ? s->g_decode.route : 0);
   g.active = true;
   return FH_OK;
 }
@@ -1343,7 +1366,7 @@ static int gen_advance(fh_session* s, int upto) {
     const int n = g.next;
     if (g.persistent && g.P + n <= C) {
       const int run = std::min(upto, 1 + g.n_dec) - n;  // cached steps are 1 .. n_dec
-      rc = s->fast.enqueue(st, fused_step(s, g.plan, 1, run));
+      rc = s->fast.enqueue(st, fused_step(s, g.plan, 1, run, g.persist_sampled, g.P + n + run - 1));
       if (rc != FH_OK) rc = set_err(rc, "fused decode launch failed: %s", hipGetErrorString(hipGetLastError()));
       g.next += run;
     } else {
@@ -1373,6 +1396,7 @@ static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, flo
     s->fast.reset();
     g.active = false;
     const unsigned what = (wait_code >> 24) & 0x7f;
+    if (what == 13 && g.persist_sampled) return kRetryPerStep;  // fh_generate repeats it on the per-step path
     if (what == 11)
       return set_err(FH_ERR_HIP, "fused decode step: a token id outside [0, VocabSize) (results discarded)");
     if (what == 12)
@@ -1391,10 +1415,10 @@ static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, flo
   return FH_OK;
 }
 
-int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
-                const double* uniforms, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
-  if (!s || !prompts || !opts || !out_ids || !out_counts) return set_err(FH_ERR_INVALID, "null argument");
-  FH_TRY(gen_setup(s, prompts, batch, P, max_new, opts, uniforms, logits_dump != nullptr));
+static int generate_once(fh_session* s, const int32_t* prompts, int batch, int P, int max_new,
+                         const fh_sampling* opts, const double* uniforms, int32_t* out_ids, int32_t* out_counts,
+                         float* logits_dump) {
+  FH_TRY(gen_setup(s, prompts, batch, P, max_new, opts, uniforms, logits_dump != nullptr, false, true));
   for (int b = 0; b < batch; b++) out_counts[b] = 0;
   if (max_new == 0) return FH_OK;
   hipStream_t st = s->ctx->stream;
@@ -1418,6 +1442,22 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
   s->n_cached = s->gen.n_dec;
   s->n_reprefill = s->gen.n_re;
   return FH_OK;
+}
+
+int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
+                const double* uniforms, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
+  if (!s || !prompts || !opts || !out_ids || !out_counts) return set_err(FH_ERR_INVALID, "null argument");
+  int rc = generate_once(s, prompts, batch, P, max_new, opts, uniforms, out_ids, out_counts, logits_dump);
+  if (rc == kRetryPerStep) {
+    // the in-kernel sampler met a case it leaves to the per-step sampler (an exact
+    // tie at a top-k threshold, a non-finite logit): the same generation again,
+    // every step drawn by the per-step sampler kernel
+    s->no_sampled_fused = true;
+    rc = generate_once(s, prompts, batch, P, max_new, opts, uniforms, out_ids, out_counts, logits_dump);
+    s->no_sampled_fused = false;
+    if (rc == FH_OK) s->route |= FH_ROUTE_RETRIED;
+  }
+  return rc;
 }
 
 int fh_generate_begin(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,

@@ -25,6 +25,7 @@ FH_DTYPE_F32 = 0
 FH_DTYPE_BF16 = 1
 # fh_last_route bits
 FH_ROUTE_FUSED_STEP, FH_ROUTE_FUSED_EPILOGUES, FH_ROUTE_ATTN_IN_PROJ, FH_ROUTE_UNFUSED = 1, 2, 4, 8
+FH_ROUTE_FUSED_SAMPLER, FH_ROUTE_RETRIED = 16, 32
 
 # Every symbol include/forge_hip.h declares (checked by the CPU tests).
 EXPORTS = (

@@ -190,6 +190,8 @@ int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t
 #define FH_ROUTE_FUSED_EPILOGUES 2  /* split-K reductions fused with the KV store and LayerNorms */
 #define FH_ROUTE_ATTN_IN_PROJ 4     /* + attention chunks combined in attn.proj's operand load */
 #define FH_ROUTE_UNFUSED 8          /* one kernel per op */
+#define FH_ROUTE_FUSED_SAMPLER 16   /* the persistent kernel also drew the sampled ids (top-k sampling) */
+#define FH_ROUTE_RETRIED 32         /* ... and met an exact top-k tie, so the generation re-ran per step */
 int fh_last_route(fh_session* s, int32_t* route);
 
 /* Sampler.ApplyRepetitionControls + Sampler.Sample on one logit row already on

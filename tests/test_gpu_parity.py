@@ -335,6 +335,12 @@ def test_c3_sampling_path(fhp, oracle, backend):
     print(f"C3: the oracle's decision on its own logits equals the GPU's id at {agree}/512 steps "
           f"(flips within the fp32 tolerance at {flips})", flush=True)
     assert agree >= 504, f"only {agree}/512 steps agree; flips at {flips}"
+    # the same generation without the logits dump draws inside the persistent kernel:
+    # the same logits and the reference's arithmetic give the same ids
+    fused = fhp.Sampler.generate(m, prompt, 512, T, K, fhp.Random(1), repetition_penalty=PEN,
+                                 no_repeat_ngram_size=NG)
+    assert route(fhp) & fhp._native.FH_ROUTE_FUSED_SAMPLER and not route(fhp) & fhp._native.FH_ROUTE_RETRIED
+    np.testing.assert_array_equal(fused, ids)
     rids, rlg = oracle.generate(oc, w, prompt, 512, temperature=T, top_k=K, uniforms=u, penalty=PEN, ngram=NG,
                                 return_logits=True)
     same = int(np.argmax(ids != rids)) if np.any(ids != rids) else 512
@@ -787,3 +793,50 @@ def test_c4_config_batch32_long_context(fhp, oracle, backend):
         for n in range(NEW):
             top = float(tf[n].max())
             assert top - float(tf[n][ids[b][n]]) <= 2 * TOL_F32 * max(1.0, abs(top)), (b, n)
+
+
+@pytest.mark.parametrize("T,k,pen,ng", [(0.7, 30, 1.1, 4), (1.0, 1, 1.0, 0), (0.8, 63, 2.0, 1), (1.3, 5, 1.0, 2),
+                                        (0.5, 40, 1.5, 0), (2.0, 12, 1.2, 3)])
+def test_in_kernel_sampler_matches_per_step_sampler(fhp, oracle, backend, T, k, pen, ng):
+    """Top-k sampling inside the persistent decode kernel (every cached step of one
+    launch draws its id from the launch's own logits) against the per-step path (the
+    fused step writes the logits, the sampler kernel draws): same ids at every step,
+    for greedy-like k = 1, the largest in-kernel k (63), penalties, n-gram bans of
+    sizes 1-4; the per-step path's ids are in turn the oracle sampler's on its logits."""
+    shape = (16384, 1024, 768, 2, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 61)
+    prompt = fhp.TrainingRandom(13).ids(shape[0], 40)
+    n = 150
+    fused = fhp.Sampler.generate(m, prompt, n, T, k, fhp.Random(5), repetition_penalty=pen, no_repeat_ngram_size=ng)
+    rt = route(fhp)
+    assert rt & fhp._native.FH_ROUTE_FUSED_SAMPLER and not rt & fhp._native.FH_ROUTE_RETRIED, rt
+    ids, lg = fhp.Sampler.generate(m, prompt, n, T, k, fhp.Random(5), repetition_penalty=pen,
+                                   no_repeat_ngram_size=ng, return_logits=True)
+    assert not route(fhp) & fhp._native.FH_ROUTE_FUSED_SAMPLER
+    np.testing.assert_array_equal(fused, ids)
+    u = fhp.Random(5).next_doubles(n)
+    seq = list(prompt)
+    for i in range(n):
+        adj = oracle.apply_repetition_controls(lg[i], seq, pen, ng) if (pen != 1.0 or ng > 0) else lg[i]
+        assert oracle.sample(adj, T, k, float(u[i])) == ids[i], i
+        seq.append(int(ids[i]))
+    m.dispose()
+
+
+def test_in_kernel_sampler_ties_repeat_the_generation_per_step(fhp, oracle, backend):
+    """A model whose logits all tie (tok_emb zero: every logit is 0) makes the in-kernel
+    sampler meet an exact tie at its top-k threshold; fh_generate then repeats the
+    generation with the per-step sampler, which keeps every tied value as the
+    reference does: the ids equal the per-step path's."""
+    shape = (16384, 1024, 768, 2, 12)
+    oc = oracle.Config(*shape)
+    w = oracle.trained_like(oc, oracle.init_weights(oc, 3), 4)
+    oracle.params(oc, w)["tok_emb"][...] = 0
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend)
+    m.load_weights(w)
+    prompt = fhp.TrainingRandom(2).ids(shape[0], 20)
+    fused = fhp.Sampler.generate(m, prompt, 30, 0.9, 20, fhp.Random(8), repetition_penalty=1.3)
+    assert route(fhp) & fhp._native.FH_ROUTE_RETRIED
+    ids = fhp.Sampler.generate(m, prompt, 30, 0.9, 20, fhp.Random(8), repetition_penalty=1.3, return_logits=True)[0]
+    np.testing.assert_array_equal(fused, ids)
+    m.dispose()
