@@ -281,10 +281,13 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
         step_bytes = decode_bytes_per_step(c, attended, batch=B)
         achieved = step_bytes / avg_step_s / 1e9
         rt = timings[-1]["route"]
-        persistent = rt == fhp._native.FH_ROUTE_FUSED_STEP and not w["sampling"]
-        if rt & fhp._native.FH_ROUTE_FUSED_STEP:
-            kernel = ("k_decode_step<768>" if persistent else
-                      "k_decode_step<768> + k_sample_row (one launch of each per sampled token)")
+        N = fhp._native
+        # one launch runs every cached step: greedy (in-kernel argmax) or top-k sampled (in-kernel draw)
+        persistent = bool(rt & N.FH_ROUTE_FUSED_STEP) and (not w["sampling"] or bool(rt & N.FH_ROUTE_FUSED_SAMPLER))
+        if persistent:
+            kernel = "k_decode_step<768, 12, sampled>" if w["sampling"] else "k_decode_step<768>"
+        elif rt & N.FH_ROUTE_FUSED_STEP:
+            kernel = "k_decode_step<768> + k_sample_row (one launch of each per sampled token)"
         else:
             kernel = "decode step graph (generic kernels)"
         tokens_per_launch = n_dec if persistent else 1

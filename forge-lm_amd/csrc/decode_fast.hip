@@ -631,24 +631,21 @@ __device__ bool gather_argmax(const B& nc, int off, unsigned tag, float& best, i
 // largest value with ties kept, exp(p - max) summed in index order, u = (float)U * sum,
 // the first index whose running sum exceeds u.
 
-__device__ __forceinline__ float wave_fmax(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float wave_fmin(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o, 64));
-  return v;
+__device__ __forceinline__ float wave_fmax(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ float wave_fmin(float v) { return -wave_max_dpp(-v); }
+// OR over the wave through the same DPP steps as wave_sum_dpp, in every lane
+__device__ __forceinline__ uint32_t wave_or_dpp(uint32_t v) {
+  int x = (int)v;
+  x |= __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x141, 0xF, 0xF, false);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x140, 0xF, 0xF, false);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);
+  x |= __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);
+  return (uint32_t)__builtin_amdgcn_readlane(x, 63);
 }
 __device__ __forceinline__ uint64_t wave_or64(uint64_t v) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    lo |= (uint32_t)__shfl_xor((int)lo, o, 64);
-    hi |= (uint32_t)__shfl_xor((int)hi, o, 64);
-  }
-  return ((uint64_t)hi << 32) | lo;
+  return ((uint64_t)wave_or_dpp((uint32_t)(v >> 32)) << 32) | wave_or_dpp((uint32_t)v);
 }
 
 // The k-th largest (duplicates counted) of the values v[j] of every lane (absent
@@ -892,7 +889,7 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
   const int r0 = lane < K ? sl.cr[lane] : 0x7fffffff;
   const float mx = wave_fmax(e0);
   int rank = 0;
-  for (int j = 0; j < K; j++) rank += sl.cr[j] < r0 ? 1 : 0;
+  for (int j = 0; j < K; j++) rank += __builtin_amdgcn_readlane(r0, j) < r0 ? 1 : 0;
   wave_lds_sync();
   if (lane < K) {
     sl.g[rank] = e0;
@@ -924,7 +921,6 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
   const NcBuf ncu(p.uc, p.uc_bytes);
   const LcBuf ncl(p.xl, p.xl_bytes);
   bool dead = false;
-  long np[7] = {0, 0, 0, 0, 0, 0, 0};  // polls per gather (trace)
   unsigned long long tfirst = 0, tdone = 0, tcomb = 0;
   auto fail = [&]() {
     dead = true;
@@ -941,7 +937,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     const unsigned tA = tb, tP = tb + 1, tC = tb + 3, tC2 = tb + 4, tD = tb + 5, tE = tb + 6, tE2 = tb + 7;
     // ---- A: x of this layer (every XCD's copy) ----
     for (int i = lane; i < S::BT; i += 64) sh.bias_s[l & 1][i] = p.btab[((size_t)l * NB + r.vb) * S::BT + i];
-    if (l > 0 && !dead && !gather<D>(ncl, r.xl0 + XL::X, tb - PH + 7, sh.xres, p.err, err_code(W_X, l), D, &np[0]))
+    if (l > 0 && !dead && !gather<D>(ncl, r.xl0 + XL::X, tb - PH + 7, sh.xres, p.err, err_code(W_X, l), D))
       fail();
     __syncthreads();
     TM(0);
@@ -953,7 +949,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     // ---- B: attention of this block's keys; publish the block's partial ----
     if (attn) {
       if (!dead && !gather<192>(ncl, r.xl0 + XL::QKV + r.hj * 192, tA, sh.qkvs, p.err, err_code(W_QKV, l), 192,
-                                &np[1]))
+                                nullptr))
         fail();
       __syncthreads();
       TM(1);
@@ -978,7 +974,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     }
     // ---- C: o of the XCD's heads from every key block's partial ----
     if (!dead &&
-        !gather_parts<D, H>(ncl, r.xl0 + XL::PARTS, r.nh, r.nkb, tP, sh.parts, p.err, err_code(W_PART, l), &np[2],
+        !gather_parts<D, H>(ncl, r.xl0 + XL::PARTS, r.nh, r.nkb, tP, sh.parts, p.err, err_code(W_PART, l), nullptr,
                             (it == r.trace_it && p.trace) ? &tfirst : nullptr))
       fail();
     if (it == r.trace_it && p.trace) tdone = wall_clock64();
@@ -1018,7 +1014,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     TM(3);
     __syncthreads();
     // ---- x2 = x + attn.proj(o) + b: this slot's columns from the 8 XCD partials ----
-    if (!dead && !gather_slices<D, RSC>(ncu, U::PX2, r.slot, tC, sh.rsv, p.err, err_code(W_PX2, l), &np[3])) fail();
+    if (!dead && !gather_slices<D, RSC>(ncu, U::PX2, r.slot, tC, sh.rsv, p.err, err_code(W_PX2, l))) fail();
     TM(7);
     wave_lds_sync();
     if (!dead && lane < RSC) {
@@ -1028,17 +1024,17 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
       const int col = r.slot * RSC + lane;
       put_pair(r.xl + XL::X2 + col, (sum + sh.bias_s[l & 1][S::B_P + lane]) + sh.xres[col], tC2);
     }
-    if (!dead && !gather<D>(ncl, r.xl0 + XL::X2, tC2, sh.x2s, p.err, err_code(W_X2, l), D, &np[4])) fail();
+    if (!dead && !gather<D>(ncl, r.xl0 + XL::X2, tC2, sh.x2s, p.err, err_code(W_X2, l), D)) fail();
     __syncthreads();
     TM(4);
     __syncthreads();
     // ---- D: the XCD's h slice ----
-    if (!dead && !gather<S::HX>(ncl, r.xl0 + XL::HH, tD, sh.hs, p.err, err_code(W_H, l), S::HX, &np[5])) fail();
+    if (!dead && !gather<S::HX>(ncl, r.xl0 + XL::HH, tD, sh.hs, p.err, err_code(W_H, l), S::HX)) fail();
     __syncthreads();
     TM(5);
     __syncthreads();
     // ---- E: x = x2 + mlp.proj(h) + b: this slot's columns from the 8 XCD partials ----
-    if (!dead && !gather_slices<D, RSC>(ncu, U::PX, r.slot, tE, sh.rsv, p.err, err_code(W_PX, l), &np[6])) fail();
+    if (!dead && !gather_slices<D, RSC>(ncu, U::PX, r.slot, tE, sh.rsv, p.err, err_code(W_PX, l))) fail();
     TM(8);
     wave_lds_sync();
     if (!dead && lane < RSC) {
@@ -1050,7 +1046,6 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     }
     TM(6);
     if (it == r.trace_it && p.trace && lane == 0) {
-      for (int i = 1; i < 3; i++) p.trace[r.blk * TRACE_PER + 9 + i] = (unsigned long long)np[i];
       p.trace[r.blk * TRACE_PER + 14] = tfirst;
       p.trace[r.blk * TRACE_PER + 15] = tcomb;
       p.trace[r.blk * TRACE_PER + 13] = tdone;
