@@ -247,9 +247,11 @@ static hipError_t launch_any(hipStream_t st, const bf16_t* a, int M, int K, cons
   // byte offsets inside a block's rows (operands and outputs) are 32-bit
   if ((size_t)256 * K * 2 > 0x7fffffffu || (size_t)256 * N * 4 > 0x7fffffffu) return hipErrorInvalidValue;
   const int gn = (N + TN - 1) / TN;
-  // 256-row tiles while they give at least one tile per CU; 128 below that
+  // 256-row tiles while they give two tiles per CU (two blocks fit a CU); 128 below
+  // that (attn.proj and mlp.proj at N 1024: 512 tiles of 128 rows instead of 256
+  // of 256, measured 2 % faster on the whole C5 forward)
   const int gm256 = (M + 255) / 256, gm128 = (M + 127) / 128;
-  if (gm256 * gn >= 256) return launch_bm<256>(st, gm256, gn, a, M, K, Wt, N, bias, epi, o);
+  if (gm256 * gn >= 512) return launch_bm<256>(st, gm256, gn, a, M, K, Wt, N, bias, epi, o);
   return launch_bm<128>(st, gm128, gn, a, M, K, Wt, N, bias, epi, o);
 }
 
