@@ -120,6 +120,7 @@ __device__ __forceinline__ unsigned xcc_id() {
 // stores (plain loads would keep hitting a stale L1 line).  Out-of-range
 // offsets read as 0.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 template <int AUX>
 struct NcBufT {
   __amdgpu_buffer_rsrc_t r;
@@ -128,6 +129,10 @@ struct NcBufT {
   __device__ __forceinline__ uint4 load4(int byte_off) const {
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, AUX);
     return make_uint4(v.x, v.y, v.z, v.w);
+  }
+  __device__ __forceinline__ uint2 load2(int byte_off) const {
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, AUX);
+    return make_uint2(v.x, v.y);
   }
 };
 #ifndef FH_LOCAL_AUX
@@ -181,7 +186,8 @@ struct Xl {
   static constexpr int HH = X2 + D;                               // the XCD's h slice
   static constexpr int X = HH + S::HX;                            // x (every XCD keeps a copy)
   static constexpr int SAMP = X + D;                              // sampler keys: 64 per block of the XCD
-  static constexpr int STRIDE = SAMP + SLOTS * 64;
+  static constexpr int SAMPT = SAMP + SLOTS * 64;                 // the two largest keys of each block
+  static constexpr int STRIDE = SAMPT + SLOTS * 2;
 };
 
 struct KParams {
@@ -555,14 +561,12 @@ struct Lds {
 template <bool SAMPLED>
 struct SampLds {
   int hist[1];
-  float g[1];
   float cv[1];
   int cr[1];
 };
 template <>
 struct SampLds<true> {
   int hist[HCAP];
-  float g[64];
   float cv[NB / NX * 64];
   int cr[NB / NX * 64];
 };
@@ -624,12 +628,13 @@ __device__ bool gather_argmax(const B& nc, int off, unsigned tag, float& best, i
 
 // ---- the sampled kernel's sampler (one wave) ----------------------------------------
 // Sampler.Sample with top-k (Sampler.cs:29-69) after ApplyRepetitionControls
-// (:111-165), spread over the launch's blocks: each block adjusts its own rows,
-// each XCD's first block selects the XCD's k largest, and every block selects the
-// k largest of the 8 XCD lists and draws.  The arithmetic is the reference's, in its
-// order: penalty (x < 0 ? x * p : x / p), division by T, the threshold = the k-th
-// largest value with ties kept, exp(p - max) summed in index order, u = (float)U * sum,
-// the first index whose running sum exceeds u.
+// (:111-165), spread over the launch's blocks: each block adjusts its own rows and
+// publishes them with its two largest values; each XCD's first block selects the
+// XCD's k largest, sorted; every block merges the 8 sorted XCD lists into the k
+// largest and draws.  The arithmetic is the reference's, in its order: penalty
+// (x < 0 ? x * p : x / p), division by T, the threshold = the k-th largest value
+// with ties kept, exp(p - max) summed in index order, u = (float)U * sum, the first
+// index whose running sum exceeds u.
 
 __device__ __forceinline__ float wave_fmax(float v) { return wave_max_dpp(v); }
 __device__ __forceinline__ float wave_fmin(float v) { return -wave_max_dpp(-v); }
@@ -646,6 +651,125 @@ __device__ __forceinline__ uint32_t wave_or_dpp(uint32_t v) {
 }
 __device__ __forceinline__ uint64_t wave_or64(uint64_t v) {
   return ((uint64_t)wave_or_dpp((uint32_t)(v >> 32)) << 32) | wave_or_dpp((uint32_t)v);
+}
+// inclusive prefix sum over the wave in lane order: shifts within rows of 16, then
+// the last lane of row 0 (2) added to row 1 (3), of row 1 to rows 2 and 3
+__device__ __forceinline__ int wave_scan_incl(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2 and 3
+  return x;
+}
+
+// ---- one-wave sorting networks: 64 entries, one per lane ----------------------
+// The value of lane ^ J: DPP for J < 16 (quad permutes, row shifts into alternate
+// 4-lane banks, row rotate by 8); for 16 and 32 the row-swap permutes, which hand
+// a lane with bit J clear its partner in the second result, a lane with it set in
+// the first (l: the lane index).
+template <int J>
+__device__ __forceinline__ int lane_xor(int v, int l) {
+  if constexpr (J == 1) {
+    return __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (J == 2) {
+    return __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (J == 4) {
+    const int a = __builtin_amdgcn_update_dpp(v, v, 0x104, 0xF, 0x5, false);  // row_shl:4 into banks 0 and 2
+    return __builtin_amdgcn_update_dpp(a, v, 0x114, 0xF, 0xA, false);        // row_shr:4 into banks 1 and 3
+  } else if constexpr (J == 8) {
+    return __builtin_amdgcn_update_dpp(v, v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (J == 16) {
+    const auto s = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)((l & 16) ? s[0] : s[1]);
+  } else {
+    static_assert(J == 32, "distance");
+    const auto s = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int)((l & 32) ? s[0] : s[1]);
+  }
+}
+// the value of lane 63 - l: mirror within rows of 16 (l ^ 15), then l ^ 16, l ^ 32
+__device__ __forceinline__ int lane_rev(int v, int l) {
+  const int m = __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return lane_xor<32>(lane_xor<16>(m, l), l);
+}
+// The lane index as a value the compiler cannot move out of the token loop: the
+// networks' per-lane masks are then recomputed where they are used instead of
+// being held (in scalar registers) for the whole kernel.
+__device__ __forceinline__ int opaque_lane() {
+  int l;
+  asm volatile("v_and_b32 %0, 63, %1" : "=v"(l) : "v"((int)threadIdx.x));
+  return l;
+}
+// 1 << 31 in the lanes where bit A of the lane index differs from bit B (B < 0: bit A set)
+__device__ __forceinline__ unsigned flip_bits(int l, int A, int B) {
+  const unsigned x = B < 0 ? (unsigned)l >> A : ((unsigned)l >> A) ^ ((unsigned)l >> B);
+  return (x & 1u) << 31;
+}
+// Compare-exchange with lane ^ J.  A lane keeps the larger value, or the smaller
+// where flip has the sign bit (comparing values with flipped signs reverses the
+// order); its payload moves with it.  A partner is taken only when strictly
+// better, so equal values stay put and no entry is lost or doubled.
+template <int J>
+__device__ __forceinline__ void cx_val(float& v, int& r, unsigned flip, int l) {
+  const float pv = __int_as_float(lane_xor<J>(__float_as_int(v), l));
+  const int pr = lane_xor<J>(r, l);
+  const bool take = __uint_as_float(__float_as_uint(pv) ^ flip) > __uint_as_float(__float_as_uint(v) ^ flip);
+  v = take ? pv : v;
+  r = take ? pr : r;
+}
+// the same for a non-negative int key kept smallest-first unless flipped (flip: 0 or ~0)
+template <int J>
+__device__ __forceinline__ void cx_key(int& k, float& v, unsigned flip, int l) {
+  const int pk = lane_xor<J>(k, l);
+  const float pv = __int_as_float(lane_xor<J>(__float_as_int(v), l));
+  const bool take = ((unsigned)pk ^ flip) < ((unsigned)k ^ flip);
+  k = take ? pk : k;
+  v = take ? pv : v;
+}
+// bitonic sort of the wave's 64 (value, row) entries, largest value in lane 0:
+// at stage (block K, distance J) a lane keeps the larger value when bits J and K
+// of its index agree
+__device__ __forceinline__ void sort64_desc(float& v, int& r) {
+  const int l = opaque_lane();
+#define FH_CX(KB, JB) cx_val<(1 << JB)>(v, r, flip_bits(l, JB, KB), l)
+  FH_CX(1, 0);
+  FH_CX(2, 1); FH_CX(2, 0);
+  FH_CX(3, 2); FH_CX(3, 1); FH_CX(3, 0);
+  FH_CX(4, 3); FH_CX(4, 2); FH_CX(4, 1); FH_CX(4, 0);
+  FH_CX(5, 4); FH_CX(5, 3); FH_CX(5, 2); FH_CX(5, 1); FH_CX(5, 0);
+  FH_CX(-1, 5); FH_CX(-1, 4); FH_CX(-1, 3); FH_CX(-1, 2); FH_CX(-1, 1); FH_CX(-1, 0);
+#undef FH_CX
+}
+// bitonic sort of 64 (key, value) entries by key, smallest key in lane 0
+__device__ __forceinline__ void sort64_key_asc(int& k, float& v) {
+  const int l = opaque_lane();
+#define FH_CX(KB, JB) cx_key<(1 << JB)>(k, v, (unsigned)((int)flip_bits(l, JB, KB) >> 31), l)
+  FH_CX(1, 0);
+  FH_CX(2, 1); FH_CX(2, 0);
+  FH_CX(3, 2); FH_CX(3, 1); FH_CX(3, 0);
+  FH_CX(4, 3); FH_CX(4, 2); FH_CX(4, 1); FH_CX(4, 0);
+  FH_CX(5, 4); FH_CX(5, 3); FH_CX(5, 2); FH_CX(5, 1); FH_CX(5, 0);
+  FH_CX(-1, 5); FH_CX(-1, 4); FH_CX(-1, 3); FH_CX(-1, 2); FH_CX(-1, 1); FH_CX(-1, 0);
+#undef FH_CX
+}
+// The 64 largest of two lists sorted largest-first (a in v/r, b in bv/br), sorted
+// largest-first into v/r: a[i] against b[63 - i] keeps the larger of each pair (a
+// bitonic sequence holding the 64 largest), then six half-cleaners sort it.
+__device__ __forceinline__ void merge64_desc(float& v, int& r, float bv, int br) {
+  const int l = opaque_lane();
+  const float rv = __int_as_float(lane_rev(__float_as_int(bv), l));
+  const int rr = lane_rev(br, l);
+  const bool take = rv > v;
+  v = take ? rv : v;
+  r = take ? rr : r;
+  cx_val<32>(v, r, flip_bits(l, 5, -1), l);
+  cx_val<16>(v, r, flip_bits(l, 4, -1), l);
+  cx_val<8>(v, r, flip_bits(l, 3, -1), l);
+  cx_val<4>(v, r, flip_bits(l, 2, -1), l);
+  cx_val<2>(v, r, flip_bits(l, 1, -1), l);
+  cx_val<1>(v, r, flip_bits(l, 0, -1), l);
 }
 
 // The k-th largest (duplicates counted) of the values v[j] of every lane (absent
@@ -780,11 +904,11 @@ __device__ void sampler_masks(const KParams& p, const int* hs, int T, int row0, 
 }
 
 // Control wave, sampled kernel, head of token t: this block's rows adjusted and
-// published; the XCD's first block selects and publishes the XCD's k largest; with
-// need_id, every block selects the k largest of the 8 XCD lists and draws the id.
-// The host only runs this kernel where no row can be all-banned and every XCD has
-// more than k unbanned rows.  Returns false after a failed wait or check (the
-// error word is set).
+// published with their two largest values; the XCD's first block selects and
+// publishes the XCD's k largest, largest first; with need_id, every block merges
+// the 8 XCD lists into the k largest and draws the id.  The host only runs this
+// kernel where no row can be all-banned and every XCD has more than k unbanned
+// rows.  Returns false after a failed wait or check (the error word is set).
 template <int D, int H>
 __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true>& sl, const Role& r, unsigned tH,
                              uint64_t pm, uint64_t bm, bool need_id, double u01, int& id) {
@@ -802,15 +926,24 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
   if ((pm >> lane) & 1ull) x = x < 0.f ? x * p.penalty : x / p.penalty;
   const float pv = (valid && !((bm >> lane) & 1ull)) ? x / p.temperature : -INFINITY;  // banned: -inf
   const unsigned tS1 = tH + 1, tS2 = tH + 2;
-  put_pair(r.xl + XL::SAMP + r.slot * 64 + lane, pv, tS1);
+  {
+    // this block's two largest values (equal when the largest repeats)
+    const float m1 = wave_fmax(pv);
+    const int l1 = (int)__builtin_ctzll(__ballot(pv == m1));
+    const float m2 = wave_fmax(lane == l1 ? -INFINITY : pv);
+    put_pair(r.xl + XL::SAMP + r.slot * 64 + lane, pv, tS1);
+    if (lane < 2) put_pair(r.xl + XL::SAMPT + r.slot * 2 + lane, lane == 0 ? m1 : m2, tS1);
+  }
   char* ucb = reinterpret_cast<char*>(p.uc);
   if (r.slot == 0) {
     // the XCD's k largest of its 32 x 64 values: pair q of the XCD's area is slot
     // q / 64, lane q % 64, i.e. row (8 (q / 64) + xcd) R + q % 64; this lane's
-    // 16-byte loads hold pairs 128 i + 2 lane and + 1
+    // 16-byte loads hold pairs 128 i + 2 lane and + 1, its 8-byte load the
+    // lane-th of the 64 block maxima
     const LcBuf ncl(p.xl, p.xl_bytes);
     float v[SLOTS];
     int rw[SLOTS];
+    float t2;
     {
       long it = 0;
       for (;;) {
@@ -818,13 +951,15 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
         uint4 a[SLOTS / 2];
 #pragma unroll
         for (int i = 0; i < SLOTS / 2; i++) a[i] = ncl.load4((r.xl0 + XL::SAMP + 128 * i + 2 * lane) * 8);
-        bool ok = true;
+        const uint2 b = ncl.load2((r.xl0 + XL::SAMPT + lane) * 8);
+        bool ok = b.y == tS1;
 #pragma unroll
         for (int i = 0; i < SLOTS / 2; i++) {
           ok &= (a[i].y == tS1) & (a[i].w == tS1);
           v[2 * i] = __uint_as_float(a[i].x);
           v[2 * i + 1] = __uint_as_float(a[i].z);
         }
+        t2 = __uint_as_float(b.x);
         if (__all(ok)) break;
         if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
           if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SKEYS, 0));
@@ -839,18 +974,59 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
           rw[2 * i + e] = ((q >> 6) * NX + r.xcd) * R + (q & 63);
         }
     }
-    int cnt = 0;
-    wave_topk<SLOTS>(v, rw, K, sl.cv, sl.cr, SLOTS * 64, &cnt);
-    if (cnt != K) {  // values tie at the XCD's k-th largest
+    // The k-th largest of the 64 block maxima bounds the XCD's k-th largest from
+    // below (they are k of the XCD's values), so the XCD's k largest are among the
+    // values >= it; when those fit one per lane they are sorted directly, else
+    // the threshold search narrows all 2048.
+    int dummy = 0;
+    sort64_desc(t2, dummy);
+    const float tau = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t2), K - 1));
+    int w = 0;
+    if (tau != -INFINITY) {
+      // each lane's candidates go to consecutive places after those of the lanes
+      // before it (a wave prefix sum of the counts); the others to a spare place
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < SLOTS; j++) c += v[j] >= tau ? 1 : 0;
+      const int incl = wave_scan_incl(c);
+      w = __builtin_amdgcn_readlane(incl, 63);
+      if (w <= 64) {
+        int pos = incl - c;
+#pragma unroll
+        for (int j = 0; j < SLOTS; j++) {
+          const bool in = v[j] >= tau;
+          const int at = in ? pos : 64 + lane;
+          sl.cv[at] = v[j];
+          sl.cr[at] = rw[j];
+          pos += in ? 1 : 0;
+        }
+      }
+    }
+    if (tau == -INFINITY || w > 64) {
+      int cnt = 0;
+      wave_topk<SLOTS>(v, rw, K, sl.cv, sl.cr, SLOTS * 64, &cnt);
+      if (cnt != K) {  // values tie at the XCD's k-th largest
+        if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
+        return false;
+      }
+      w = K;
+    }
+    wave_lds_sync();
+    float e = lane < w ? sl.cv[lane] : -INFINITY;
+    int er = lane < w ? sl.cr[lane] : 0x7fffffff;
+    sort64_desc(e, er);
+    // values tie at the XCD's k-th largest (K <= 63, so lane K exists)
+    if (__builtin_amdgcn_readlane(__float_as_int(e), K) == __builtin_amdgcn_readlane(__float_as_int(e), K - 1)) {
       if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
       return false;
     }
+    wave_lds_sync();  // every lane has read its candidate before the next token's writes
     if (lane < K)
       *reinterpret_cast<uint4*>(ucb + p.off_slist + (r.xcd * 64 + lane) * 16) =
-          make_uint4(__float_as_uint(sl.cv[lane]), (unsigned)sl.cr[lane], tS2, tS2);
+          make_uint4(__float_as_uint(e), (unsigned)er, tS2, tS2);
   }
   if (!need_id) return true;
-  // the k largest of the 8 XCD lists (record j: list j / K, entry j % K)
+  // lane i holds entry i of every XCD list (lists are largest-first; lanes >= K -inf)
   const NcBuf ncu(p.uc, p.uc_bytes);
   float g[NX];
   int gr[NX];
@@ -859,17 +1035,13 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
     reload_fence();
     uint4 a[NX];
 #pragma unroll
-    for (int i = 0; i < NX; i++) {
-      const int j = min(i * 64 + lane, NX * K - 1);
-      a[i] = ncu.load4(p.off_slist + ((j / K) * 64 + j % K) * 16);
-    }
+    for (int i = 0; i < NX; i++) a[i] = ncu.load4(p.off_slist + (i * 64 + min(lane, K - 1)) * 16);
     bool ok = true;
 #pragma unroll
     for (int i = 0; i < NX; i++) {
-      const bool in = i * 64 + lane < NX * K;
-      ok &= !in || ((a[i].z == tS2) & (a[i].w == tS2));
-      g[i] = in ? __uint_as_float(a[i].x) : -INFINITY;
-      gr[i] = (int)a[i].y;
+      ok &= lane >= K || ((a[i].z == tS2) & (a[i].w == tS2));
+      g[i] = lane < K ? __uint_as_float(a[i].x) : -INFINITY;
+      gr[i] = lane < K ? (int)a[i].y : 0x7fffffff;
     }
     if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
@@ -877,27 +1049,25 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
       return false;
     }
   }
-  int cnt = 0;
-  wave_topk<NX>(g, gr, K, sl.cv, sl.cr, NX * 64, &cnt);
-  if (cnt != K) {  // values tie at the k-th largest: the reference keeps them all
+  // the 64 largest of the 8 lists, largest first: a tree of pairwise merges
+  merge64_desc(g[0], gr[0], g[1], gr[1]);
+  merge64_desc(g[2], gr[2], g[3], gr[3]);
+  merge64_desc(g[4], gr[4], g[5], gr[5]);
+  merge64_desc(g[6], gr[6], g[7], gr[7]);
+  merge64_desc(g[0], gr[0], g[2], gr[2]);
+  merge64_desc(g[4], gr[4], g[6], gr[6]);
+  merge64_desc(g[0], gr[0], g[4], gr[4]);
+  if (__builtin_amdgcn_readlane(__float_as_int(g[0]), K) == __builtin_amdgcn_readlane(__float_as_int(g[0]), K - 1)) {
+    // values tie at the k-th largest: the reference keeps them all
     if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
     return false;
   }
-  // the kept values, their maximum, and their order by row (Sampler.cs:52-68 walks
-  // the rows in index order: the exps summed one by one, the first row past u)
-  const float e0 = lane < K ? sl.cv[lane] : -INFINITY;
-  const int r0 = lane < K ? sl.cr[lane] : 0x7fffffff;
-  const float mx = wave_fmax(e0);
-  int rank = 0;
-  for (int j = 0; j < K; j++) rank += __builtin_amdgcn_readlane(r0, j) < r0 ? 1 : 0;
-  wave_lds_sync();
-  if (lane < K) {
-    sl.g[rank] = e0;
-    sl.cr[SLOTS * 32 + rank] = r0;
-  }
-  wave_lds_sync();
-  const float ps = lane < K ? sl.g[lane] : -INFINITY;
-  const int rs = lane < K ? sl.cr[SLOTS * 32 + lane] : 0;
+  // the kept values in row order (Sampler.cs:52-68 walks the rows in index order:
+  // the exps summed one by one, the first row past u)
+  const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g[0]), 0));
+  int rs = lane < K ? gr[0] : 0x7fffffff;
+  float ps = lane < K ? g[0] : 0.f;
+  sort64_key_asc(rs, ps);
   const float ex = lane < K ? expf(ps - mx) : 0.f;
   float acc = 0.f, pre = 0.f;
   for (int j = 0; j < K; j++) {
@@ -1068,6 +1238,13 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
       const unsigned tH = tbase + PH * p.L;
       if constexpr (SAMPLED) {
         const bool next = t + 1 < p.nsteps;
+        // the next position's embedding row does not depend on the draw: fetched first
+        float4 pe4[S::KC];
+        if (next) {
+          const float* pe = p.pos + (size_t)(r.pos0 + t + 1) * D;
+#pragma unroll
+          for (int c = 0; c < S::KC; c++) pe4[c] = *reinterpret_cast<const float4*>(pe + c * 256 + lane * 4);
+        }
         int bi = 0;
         if (!dead && !sampler_draw<D, H>(p, sh, sl, r, tH, pmask, bmask, next || r.blk == 0, u01, bi)) fail();
         if (!dead && (next || r.blk == 0)) {
@@ -1075,19 +1252,20 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
           if (r.blk == 0 && lane == 0) {
             p.tokens_out[p.src.tok_off + 1 + n] = bi;  // window position prompt_len + n
             if (n < p.max_new) p.out_ids[n] = bi;
-            if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+            if (p.eos >= 0 && bi == p.eos && p.out_counts[0] < 0) p.out_counts[0] = n + 1;
             *p.step_out = n + 1;
           }
           if (next) {
             if (lane == 0) sl.hist[r.nh0 + t] = bi;  // the window grows by the drawn id
             const float* te = p.tok + (size_t)bi * D;
-            const float* pe = p.pos + (size_t)(r.pos0 + t + 1) * D;
+            float4 a[S::KC];
+#pragma unroll
+            for (int c = 0; c < S::KC; c++) a[c] = *reinterpret_cast<const float4*>(te + c * 256 + lane * 4);
 #pragma unroll
             for (int c = 0; c < S::KC; c++) {
-              const int i = c * 256 + lane * 4;
-              const float4 a = *reinterpret_cast<const float4*>(te + i);
-              const float4 b = *reinterpret_cast<const float4*>(pe + i);
-              *reinterpret_cast<float4*>(sh.xres + i) = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+              const float4 b = pe4[c];
+              *reinterpret_cast<float4*>(sh.xres + c * 256 + lane * 4) =
+                  make_float4(a[c].x + b.x, a[c].y + b.y, a[c].z + b.z, a[c].w + b.w);
             }
           }
         }
@@ -1128,7 +1306,7 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
           if (r.blk == 0 && lane == 0 && p.greedy) {
             p.tokens_out[p.src.tok_off + 1 + n] = bi;  // window position prompt_len + n
             if (n < p.max_new) p.out_ids[n] = bi;
-            if (p.out_counts[0] < 0 && p.eos >= 0 && bi == p.eos) p.out_counts[0] = n + 1;
+            if (p.eos >= 0 && bi == p.eos && p.out_counts[0] < 0) p.out_counts[0] = n + 1;
             *p.step_out = n + 1;
           }
           if (thead) trace_mark(p.trace, 18);
