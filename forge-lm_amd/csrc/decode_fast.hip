@@ -571,6 +571,37 @@ struct SampLds<true> {
   int cr[NB / NX * 64];
 };
 
+// The tied head's rows, per data wave (rows w, w + 3, ... of the block's share).
+// ROWS of them stay in LDS for the whole launch (the table does not change
+// between steps, so they are read from HBM once per launch instead of once per
+// token; 12 fill the LDS the sampled kernel leaves); INFLIGHT of the rest stream
+// from HBM at a time.  Both are measured per kernel: the greedy kernel streams
+// every row three at a time (holding rows in LDS shortened its head but slowed
+// its layers by more), the sampled kernel holds 12 and streams two at a time.
+#ifndef FH_HRES_G
+#define FH_HRES_G 0
+#endif
+#ifndef FH_HRES_S
+#define FH_HRES_S 12
+#endif
+#ifndef FH_HG_G
+#define FH_HG_G 3
+#endif
+#ifndef FH_HG_S
+#define FH_HG_S 2
+#endif
+template <bool SAMPLED>
+struct HeadRes {
+  static constexpr int ROWS = SAMPLED ? FH_HRES_S : FH_HRES_G;
+  static constexpr int INFLIGHT = SAMPLED ? FH_HG_S : FH_HG_G;
+};
+// the LDS rows (only kernels that hold some instantiate it)
+template <int N>
+__device__ __forceinline__ float* head_rows_lds() {
+  __shared__ __align__(16) float rows[N];
+  return rows;
+}
+
 // What this block and wave do in the step
 struct Role {
   int blk, w, lane, xcd, slot, vb;
@@ -1348,9 +1379,6 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
 // puts, at the start of B and after B (attention blocks), after the puts of
 // C, D and E.  A tile requested before its use in the layer is the layer's
 // own; after its use, the next layer's (the next token's first after the last).
-#ifndef FH_HG
-#define FH_HG 3
-#endif
 enum Site : int { S_AEND = 0, S_BSTART = 1, S_BEND = 2, S_CEND = 3, S_DEND = 4, S_EEND = 5 };
 // site of each tile: non-attention blocks request mlp.fc / mlp.proj / next qkv
 // right after A (their only slack is the attention window); attention blocks
@@ -1452,6 +1480,31 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
   __syncthreads(); \
   dead = sh.fail != 0
   bool dead = false;
+  constexpr int NPF = HeadRes<SAMPLED>::ROWS;
+  if constexpr (NPF > 0) {
+    // the first NPF head rows this wave owns (w, w + 3, ... of the block's share)
+    // are copied to LDS once; launches of one step read every row from HBM
+    const int R = p.Vp / NB;
+    const float* E = p.tok + (size_t)(SAMPLED ? r.vb : r.blk) * R * D;
+    const int npf = p.nsteps > 1 ? min((R - w + NDW - 1) / NDW, NPF) : 0;
+    float* hw = head_rows_lds<NDW * NPF * D>() + (size_t)w * NPF * D;
+    for (int u0 = 0; u0 < npf; u0 += 4) {
+      float4 hv[4 * KC];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int row = w + NDW * min(u0 + u, npf - 1);
+#pragma unroll
+        for (int c = 0; c < KC; c++)
+          hv[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (u0 + u < npf)
+#pragma unroll
+          for (int c = 0; c < KC; c++)
+            *reinterpret_cast<float4*>(hw + (size_t)(u0 + u) * D + c * 256 + lane * 4) = hv[u * KC + c];
+    }
+  }
   // Iteration l = -1 only requests layer 0's tiles, through the same load
   // statements as every later layer: each tile register has a single load
   // site, so no copy of an in-flight register (and no wait for it) is needed.
@@ -1701,15 +1754,18 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
       // 256 * R rows when V is not a multiple of 256; rows >= V are left out of the
       // argmax); R >= 3, so every data wave has rows: w, w+3, ...
       const int R = p.Vp / NB;
-      constexpr int HG = FH_HG;  // rows per wave in flight
+      constexpr int HG = HeadRes<SAMPLED>::INFLIGHT;  // rows per wave in flight
       // (the sampled kernel gives block vb the rows of vb: an XCD's blocks know each other's rows)
       const float* E = p.tok + (size_t)(SAMPLED ? r.vb : r.blk) * R * D;
       const int nrow = (R - w + NDW - 1) / NDW;
-      // the first rows are requested before the final x arrives
+      // the first npf rows are in LDS; rows npf .. nrow - 1 stream from HBM, the
+      // first of them requested before the final x arrives
+      const int npf = NPF > 0 && p.nsteps > 1 ? min(nrow, NPF) : 0;
+      const float* hw = NPF > 0 ? head_rows_lds<NDW * (NPF > 0 ? NPF : 1) * D>() + (size_t)w * NPF * D : nullptr;
       float4 rh[HG * KC];
 #pragma unroll
       for (int u = 0; u < HG; u++) {
-        const int row = w + NDW * min(u, nrow - 1);
+        const int row = w + NDW * min(npf + u, nrow - 1);
 #pragma unroll
         for (int c = 0; c < KC; c++)
           rh[u * KC + c] = *reinterpret_cast<const float4*>(E + (size_t)row * D + c * 256 + lane * 4);
@@ -1727,7 +1783,16 @@ __device__ __forceinline__ void data_loop(const KParams& p, Lds<D, H>& sh, Role 
           }
           ln_lane<KC, D>(sh.xres, lw, lb, xn);
         }
-        for (int g = 0; g < nrow; g += HG) {
+        // the rows held in LDS first: their arithmetic covers the streamed rows' latency
+        for (int u = 0; u < npf; u++) {
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < KC; c++)
+            acc += dot4(*reinterpret_cast<const float4*>(hw + (size_t)u * D + c * 256 + lane * 4), xn[c]);
+          const float v = wave_sum_dpp(acc);
+          if (lane == 0) sh.hval[w + NDW * u] = v;
+        }
+        for (int g = npf; g < nrow; g += HG) {
           float4 nx[HG * KC];
 #pragma unroll
           for (int u = 0; u < HG; u++) {
