@@ -483,8 +483,9 @@ __device__ bool gather_parts_r(const B& nc, int pair0, int nh, int nkb, unsigned
   constexpr int Q = PART / 2;  // 16-byte loads per partial
   const int lane = threadIdx.x & 63;
   const int per = nkb * Q, n = nh * per;
-  // byte offset of each of this lane's loads (clamped into range; the extra
-  // lanes re-read the last unit and are not checked)
+  // byte offset of each of this lane's loads, clamped into range: the extra
+  // lanes re-read the last unit, check its tags and store its values again, so
+  // no per-lane condition (held in scalar registers) is needed
   int off[RA];
 #pragma unroll
   for (int i = 0; i < RA; i++) {
@@ -499,8 +500,7 @@ __device__ bool gather_parts_r(const B& nc, int pair0, int nh, int nkb, unsigned
     for (int i = 0; i < RA; i++) v[i] = nc.load4(off[i]);
     bool ok = true;
 #pragma unroll
-    for (int i = 0; i < RA; i++)
-      if (i * 64 + lane < n) ok &= (v[i].y == tag) & (v[i].w == tag);
+    for (int i = 0; i < RA; i++) ok &= (v[i].y == tag) & (v[i].w == tag);
     if (tfirst && it == 0) *tfirst = wall_clock64();
     if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(err))) {
@@ -511,12 +511,9 @@ __device__ bool gather_parts_r(const B& nc, int pair0, int nh, int nkb, unsigned
   if (npoll) *npoll = it;
 #pragma unroll
   for (int i = 0; i < RA; i++) {
-    const int u = i * 64 + lane;
-    if (u < n) {
-      const int j = u / per, q = u - j * per;
-      *reinterpret_cast<float2*>(out + j * S::SPH * PART + 2 * q) =
-          make_float2(__uint_as_float(v[i].x), __uint_as_float(v[i].z));
-    }
+    const int u = min(i * 64 + lane, n - 1), j = u / per, q = u - j * per;
+    *reinterpret_cast<float2*>(out + j * S::SPH * PART + 2 * q) =
+        make_float2(__uint_as_float(v[i].x), __uint_as_float(v[i].z));
   }
   return true;
 }
