@@ -1064,14 +1064,18 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
     uint4 a[NX];
 #pragma unroll
     for (int i = 0; i < NX; i++) a[i] = ncu.load4(p.off_slist + (i * 64 + min(lane, K - 1)) * 16);
+    // lanes past K re-read entry K - 1 and check it too (no per-lane condition)
     bool ok = true;
 #pragma unroll
-    for (int i = 0; i < NX; i++) {
-      ok &= lane >= K || ((a[i].z == tS2) & (a[i].w == tS2));
-      g[i] = lane < K ? __uint_as_float(a[i].x) : -INFINITY;
-      gr[i] = lane < K ? (int)a[i].y : 0x7fffffff;
+    for (int i = 0; i < NX; i++) ok &= (a[i].z == tS2) & (a[i].w == tS2);
+    if (__all(ok)) {
+#pragma unroll
+      for (int i = 0; i < NX; i++) {
+        g[i] = lane < K ? __uint_as_float(a[i].x) : -INFINITY;
+        gr[i] = lane < K ? (int)a[i].y : 0x7fffffff;
+      }
+      break;
     }
-    if (__all(ok)) break;
     if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
       if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SLIST, 0));
       return false;
