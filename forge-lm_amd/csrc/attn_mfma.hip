@@ -33,7 +33,7 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + (lane >> 5) * 4 + (r & 3); }
 
-__device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__bf16, f32_to_bf16(f)); }
+__device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__bf16, bf16_rn(f)); }
 
 template <typename KT, typename OT, typename QT>
 __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict__ qp, int qstride, int T, int d, int H,
@@ -232,8 +232,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
       const float4 v = make_float4(ot[dt][4 * g] * inv, ot[dt][4 * g + 1] * inv, ot[dt][4 * g + 2] * inv,
                                    ot[dt][4 * g + 3] * inv);
       if constexpr (sizeof(OT) == 2) {
-        const uint32_t lo = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+        const uint32_t lo = (uint32_t)bf16_rn(v.x) | ((uint32_t)bf16_rn(v.y) << 16);
+        const uint32_t hi = (uint32_t)bf16_rn(v.z) | ((uint32_t)bf16_rn(v.w) << 16);
         *reinterpret_cast<uint2*>(orow + dt * 32 + 8 * g + 4 * half) = make_uint2(lo, hi);
       } else {
         *reinterpret_cast<float4*>(orow + dt * 32 + 8 * g + 4 * half) = v;

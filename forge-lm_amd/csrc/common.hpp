@@ -26,6 +26,10 @@ __device__ __host__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return (bf16_t)(u >> 16);
 }
 
+// The same rounding on the device: one v_cvt_pk_bf16_f32 (round to nearest even,
+// the bits of f32_to_bf16 for every value that is not a NaN).
+__device__ __forceinline__ bf16_t bf16_rn(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+
 template <typename T>
 __device__ __forceinline__ float to_f32(T v);
 template <>
@@ -38,7 +42,7 @@ __device__ __forceinline__ T from_f32(float v);
 template <>
 __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 template <>
-__device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return f32_to_bf16(v); }
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return bf16_rn(v); }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

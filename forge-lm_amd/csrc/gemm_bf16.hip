@@ -177,7 +177,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_bf16(const bf16_t* __restrict__
           for (int r = 0; r < 16; r++) {
             float v = acc[2 * half + ii][j][r] + bcol[j];
             if constexpr (EPI == EPI_GELU) v = gelu_for_bf16(v);
-            stg[(ii * 32 + mfma_acc_row(lane, r)) * SROW + j * 32 + fr] = f32_to_bf16(v);
+            stg[(ii * 32 + mfma_acc_row(lane, r)) * SROW + j * 32 + fr] = bf16_rn(v);
           }
 #pragma unroll
       for (int it = 0; it < 8; it++) {

@@ -152,8 +152,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
     for (int i = 0; i < AV; i++) {
       const int idx = tid + 256 * i, row = idx / (BK / 4), kq = idx % (BK / 4);
       if constexpr (sizeof(WT) == 2) {
-        const uint32_t lo = (uint32_t)f32_to_bf16(a[i].x) | ((uint32_t)f32_to_bf16(a[i].y) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16(a[i].z) | ((uint32_t)f32_to_bf16(a[i].w) << 16);
+        const uint32_t lo = (uint32_t)bf16_rn(a[i].x) | ((uint32_t)bf16_rn(a[i].y) << 16);
+        const uint32_t hi = (uint32_t)bf16_rn(a[i].z) | ((uint32_t)bf16_rn(a[i].w) << 16);
         *reinterpret_cast<uint2*>(&As[b][row][4 * kq]) = make_uint2(lo, hi);
       } else {
         // k = 4kq .. 4kq+3: even k to positions 2kq, 2kq+1; odd k to BK/2 + 2kq, +1

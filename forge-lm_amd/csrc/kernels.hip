@@ -144,10 +144,10 @@ __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __rest
   for (int i = 0; i < VPL; i++) {
     const float4 wv = reinterpret_cast<const float4*>(w)[i * 64 + lane];
     const float4 bv = reinterpret_cast<const float4*>(b)[i * 64 + lane];
-    const uint32_t lo = (uint32_t)f32_to_bf16(x[i].x * rs * wv.x + bv.x) |
-                        ((uint32_t)f32_to_bf16(x[i].y * rs * wv.y + bv.y) << 16);
-    const uint32_t hi = (uint32_t)f32_to_bf16(x[i].z * rs * wv.z + bv.z) |
-                        ((uint32_t)f32_to_bf16(x[i].w * rs * wv.w + bv.w) << 16);
+    const uint32_t lo = (uint32_t)bf16_rn(x[i].x * rs * wv.x + bv.x) |
+                        ((uint32_t)bf16_rn(x[i].y * rs * wv.y + bv.y) << 16);
+    const uint32_t hi = (uint32_t)bf16_rn(x[i].z * rs * wv.z + bv.z) |
+                        ((uint32_t)bf16_rn(x[i].w * rs * wv.w + bv.w) << 16);
     orow[i * 64 + lane] = make_uint2(lo, hi);
   }
 }
@@ -1312,7 +1312,7 @@ __global__ void k_copy_bytes(const uint4* __restrict__ src, uint4* __restrict__ 
 // out[i] = bf16(in[i]), nearest-even, over a grid-stride loop
 __global__ void k_round_bf16(const float* __restrict__ in, bf16_t* __restrict__ out, size_t n) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = f32_to_bf16(in[i]);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) out[i] = bf16_rn(in[i]);
 }
 
 // ---------------------------------------------------------------------------

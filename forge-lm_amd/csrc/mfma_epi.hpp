@@ -52,7 +52,7 @@ __device__ __forceinline__ void mfma_store_tile(const mfma_f32x16_t& acc, int la
     if constexpr (RES) s += rv[r];
     const int e = (trow0 + mfma_acc_row(lane, r)) * N + col;
     if constexpr (OUT_BF16)
-      __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(s), ry, e * 2, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b16(bf16_rn(s), ry, e * 2, 0, 0);
     else
       __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, s), ry, e * 4, 0, 0);
   }
