@@ -417,6 +417,34 @@ def test_matmul_nn_matches_oracle(fhp, oracle, backend, M, K, N, dtype):
         buf.free()
 
 
+def test_bf16_operand_rounding_is_nearest_even_bit_for_bit(fhp, backend):
+    """The device rounds a to bf16 before the bf16 GEMM (hardware convert); with an
+    identity weight the product returns the rounded operand, which must equal the
+    software round-to-nearest-even bit for bit, halfway cases and signs included
+    (normal values only: the MFMA treats denormal operands as zero)."""
+    M, K, N = 256, 64, 64
+    r = np.random.default_rng(7)
+    hi = r.integers(0x0080, 0x7F00, size=(M, K)).astype(np.uint32)  # normal exponents, either sign below
+    lo = r.integers(0, 0x10000, size=(M, K)).astype(np.uint32)
+    lo[:, 0::4] = 0x8000  # exact halfway: ties to even
+    lo[:, 1::4] = 0x7FFF
+    lo[:, 2::8] = 0x8001
+    sign = (r.integers(0, 2, size=(M, K)).astype(np.uint32) << 31)
+    a = ((hi << 16) | lo | sign).view(np.float32)
+    a[0, :8] = [0.0, -0.0, 1.0, -1.0, 3.0e38, -3.0e38, 1.5, 65504.0]
+    eye = np.eye(K, N, dtype=np.float32)
+    _, eye_bits = bf16_round(eye)
+    bufa = fhp.DeviceBuffer.from_array(backend, a)
+    bufb = fhp.DeviceBuffer.from_array(backend, eye_bits)
+    bufy = fhp.DeviceBuffer.from_array(backend, np.zeros((M, N), np.float32))
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=False, dtype="bf16")
+    got = bufy.read(np.float32, M * N).reshape(M, N)
+    want, _ = bf16_round(a)
+    assert np.array_equal(got, want), int(np.sum(got != want))
+    for buf in (bufa, bufb, bufy):
+        buf.free()
+
+
 @pytest.mark.parametrize("M,K,N", [(2000, 512, 4000), (256, 4096, 1024), (8192, 1024, 256)])
 def test_matmul_nn_bf16_large_tiles(fhp, backend, M, K, N):
     # bf16 products of 256 rows or more run on the bf16-operand GEMM of the window
