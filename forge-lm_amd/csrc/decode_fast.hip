@@ -693,6 +693,8 @@ __device__ __forceinline__ int wave_scan_incl(int x) {
 }
 
 // ---- one-wave sorting networks: 64 entries, one per lane ----------------------
+// (used by the sampled kernel only; marks what the greedy
+// kernel's translation unit, decode_fast.hip itself, leaves out)
 // The value of lane ^ J: DPP for J < 16 (quad permutes, row shifts into alternate
 // 4-lane banks, row rotate by 8); for 16 and 32 the row-swap permutes, which hand
 // a lane with bit J clear its partner in the second result, a lane with it set in
@@ -739,13 +741,16 @@ __device__ __forceinline__ unsigned flip_bits(int l, int A, int B) {
 // where flip has the sign bit (comparing values with flipped signs reverses the
 // order); its payload moves with it.  A partner is taken only when strictly
 // better, so equal values stay put and no entry is lost or doubled.
-template <int J>
+// (PAY false: the value alone, r untouched)
+template <int J, bool PAY = true>
 __device__ __forceinline__ void cx_val(float& v, int& r, unsigned flip, int l) {
   const float pv = __int_as_float(lane_xor<J>(__float_as_int(v), l));
-  const int pr = lane_xor<J>(r, l);
   const bool take = __uint_as_float(__float_as_uint(pv) ^ flip) > __uint_as_float(__float_as_uint(v) ^ flip);
   v = take ? pv : v;
-  r = take ? pr : r;
+  if constexpr (PAY) {
+    const int pr = lane_xor<J>(r, l);
+    r = take ? pr : r;
+  }
 }
 // the same for a non-negative int key kept smallest-first unless flipped (flip: 0 or ~0)
 template <int J>
@@ -758,10 +763,11 @@ __device__ __forceinline__ void cx_key(int& k, float& v, unsigned flip, int l) {
 }
 // bitonic sort of the wave's 64 (value, row) entries, largest value in lane 0:
 // at stage (block K, distance J) a lane keeps the larger value when bits J and K
-// of its index agree
+// of its index agree (PAY false: the values alone)
+template <bool PAY = true>
 __device__ __forceinline__ void sort64_desc(float& v, int& r) {
   const int l = opaque_lane();
-#define FH_CX(KB, JB) cx_val<(1 << JB)>(v, r, flip_bits(l, JB, KB), l)
+#define FH_CX(KB, JB) cx_val<(1 << JB), PAY>(v, r, flip_bits(l, JB, KB), l)
   FH_CX(1, 0);
   FH_CX(2, 1); FH_CX(2, 0);
   FH_CX(3, 2); FH_CX(3, 1); FH_CX(3, 0);
@@ -770,8 +776,11 @@ __device__ __forceinline__ void sort64_desc(float& v, int& r) {
   FH_CX(-1, 5); FH_CX(-1, 4); FH_CX(-1, 3); FH_CX(-1, 2); FH_CX(-1, 1); FH_CX(-1, 0);
 #undef FH_CX
 }
-// bitonic sort of 64 (key, value) entries by key, smallest key in lane 0
-__device__ __forceinline__ void sort64_key_asc(int& k, float& v) {
+// bitonic sort of (key, value) entries by key: W 32 sorts lanes 0..31 smallest
+// key first (and 32..63 largest first), W 64 the whole wave smallest key first
+template <int W>
+__device__ __forceinline__ void sort_key_asc(int& k, float& v) {
+  static_assert(W == 32 || W == 64, "width");
   const int l = opaque_lane();
 #define FH_CX(KB, JB) cx_key<(1 << JB)>(k, v, (unsigned)((int)flip_bits(l, JB, KB) >> 31), l)
   FH_CX(1, 0);
@@ -779,7 +788,9 @@ __device__ __forceinline__ void sort64_key_asc(int& k, float& v) {
   FH_CX(3, 2); FH_CX(3, 1); FH_CX(3, 0);
   FH_CX(4, 3); FH_CX(4, 2); FH_CX(4, 1); FH_CX(4, 0);
   FH_CX(5, 4); FH_CX(5, 3); FH_CX(5, 2); FH_CX(5, 1); FH_CX(5, 0);
-  FH_CX(-1, 5); FH_CX(-1, 4); FH_CX(-1, 3); FH_CX(-1, 2); FH_CX(-1, 1); FH_CX(-1, 0);
+  if constexpr (W == 64) {
+    FH_CX(-1, 5); FH_CX(-1, 4); FH_CX(-1, 3); FH_CX(-1, 2); FH_CX(-1, 1); FH_CX(-1, 0);
+  }
 #undef FH_CX
 }
 // The 64 largest of two lists sorted largest-first (a in v/r, b in bv/br), sorted
@@ -798,6 +809,44 @@ __device__ __forceinline__ void merge64_desc(float& v, int& r, float bv, int br)
   cx_val<4>(v, r, flip_bits(l, 2, -1), l);
   cx_val<2>(v, r, flip_bits(l, 1, -1), l);
   cx_val<1>(v, r, flip_bits(l, 0, -1), l);
+}
+// the value of lane l ^ 31 (each 32-lane half reversed): row mirror, then l ^ 16
+__device__ __forceinline__ int lane_rev32(int v, int l) {
+  const int m = __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  return lane_xor<16>(m, l);
+}
+// Lists of 32 entries, one per 32-lane half, each sorted largest-first.  Each half
+// of v/r becomes the 32 largest of its own list and the list in the same half of
+// bv/br (FOLD false), or of its list and the other half's (FOLD true, bv/br =
+// v/r), sorted largest-first: entry i against the other list's entry 31 - i keeps
+// the larger of each pair (a bitonic sequence holding the 32 largest), then five
+// half-cleaners within the half sort it.
+template <bool FOLD>
+__device__ __forceinline__ void merge32_desc(float& v, int& r, float bv, int br) {
+  const int l = opaque_lane();
+  const float rv = __int_as_float(FOLD ? lane_rev(__float_as_int(bv), l) : lane_rev32(__float_as_int(bv), l));
+  const int rr = FOLD ? lane_rev(br, l) : lane_rev32(br, l);
+  const bool take = rv > v;
+  v = take ? rv : v;
+  r = take ? rr : r;
+  cx_val<16>(v, r, flip_bits(l, 4, -1), l);
+  cx_val<8>(v, r, flip_bits(l, 3, -1), l);
+  cx_val<4>(v, r, flip_bits(l, 2, -1), l);
+  cx_val<2>(v, r, flip_bits(l, 1, -1), l);
+  cx_val<1>(v, r, flip_bits(l, 0, -1), l);
+}
+// Running sums in lane order with the rounding of a sequential loop: lane j gets
+// (((v_0 + v_1) + v_2) + ... ) + v_j for j < W.  Each step shifts the sums one
+// lane up the whole wave (DPP wave_shr:1; lane 0 receives 0) and adds the lane's
+// own value, so after step s lanes 0..s hold their final sums.  Exact for
+// non-negative values (lanes past the entries should hold 0).
+template <int W>
+__device__ __forceinline__ float seq_prefix(float v) {
+  float a = v;
+#pragma unroll
+  for (int s = 1; s < W; s++)
+    a = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(a), 0x138, 0xF, 0xF, true));
+  return a;
 }
 
 // The k-th largest (duplicates counted) of the values v[j] of every lane (absent
@@ -931,6 +980,44 @@ __device__ void sampler_masks(const KParams& p, const int* hs, int T, int row0, 
   }
 }
 
+// The 8 published XCD lists (k entries each, largest first, tag `tag`), NR per
+// lane: NR 8 puts entry l of list i in lane l of g[i]; NR 4 puts two lists in a
+// register, entry l % 32 of list 2 i + l / 32 in lane l (k < 32).  Entries past k
+// are -inf (row INT_MAX); lanes past k re-read entry k - 1 and check it too.
+template <int NR>
+__device__ __forceinline__ bool gather_slists(const NcBuf& nc, const KParams& p, int K, unsigned tag, float* g,
+                                              int* gr) {
+  static_assert(NR == NX || NR == NX / 2, "lists per register");
+  const int lane = threadIdx.x & 63;
+  const int e = NR == NX ? lane : (lane & 31);
+  const int ec = min(e, K - 1);
+  long it = 0;
+  for (;;) {
+    reload_fence();
+    uint4 a[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) {
+      const int list = NR == NX ? i : 2 * i + (lane >> 5);
+      a[i] = nc.load4(p.off_slist + (list * 64 + ec) * 16);
+    }
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < NR; i++) ok &= (a[i].z == tag) & (a[i].w == tag);
+    if (__all(ok)) {
+#pragma unroll
+      for (int i = 0; i < NR; i++) {
+        g[i] = e < K ? __uint_as_float(a[i].x) : -INFINITY;
+        gr[i] = e < K ? (int)a[i].y : 0x7fffffff;
+      }
+      return true;
+    }
+    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
+      if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SLIST, 0));
+      return false;
+    }
+  }
+}
+
 // Control wave, sampled kernel, head of token t: this block's rows adjusted and
 // published with their two largest values; the XCD's first block selects and
 // publishes the XCD's k largest, largest first; with need_id, every block merges
@@ -1007,7 +1094,7 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
     // values >= it; when those fit one per lane they are sorted directly, else
     // the threshold search narrows all 2048.
     int dummy = 0;
-    sort64_desc(t2, dummy);
+    sort64_desc<false>(t2, dummy);
     const float tau = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(t2), K - 1));
     int w = 0;
     if (tau != -INFINITY) {
@@ -1054,58 +1141,53 @@ __device__ bool sampler_draw(const KParams& p, const Lds<D, H>& sh, SampLds<true
           make_uint4(__float_as_uint(e), (unsigned)er, tS2, tS2);
   }
   if (!need_id) return true;
-  // lane i holds entry i of every XCD list (lists are largest-first; lanes >= K -inf)
+  // the k + 1 largest of the 8 lists, largest first, in lanes 0..k of g0/r0
   const NcBuf ncu(p.uc, p.uc_bytes);
-  float g[NX];
-  int gr[NX];
-  long it = 0;
-  for (;;) {
-    reload_fence();
-    uint4 a[NX];
-#pragma unroll
-    for (int i = 0; i < NX; i++) a[i] = ncu.load4(p.off_slist + (i * 64 + min(lane, K - 1)) * 16);
-    // lanes past K re-read entry K - 1 and check it too (no per-lane condition)
-    bool ok = true;
-#pragma unroll
-    for (int i = 0; i < NX; i++) ok &= (a[i].z == tS2) & (a[i].w == tS2);
-    if (__all(ok)) {
-#pragma unroll
-      for (int i = 0; i < NX; i++) {
-        g[i] = lane < K ? __uint_as_float(a[i].x) : -INFINITY;
-        gr[i] = lane < K ? (int)a[i].y : 0x7fffffff;
-      }
-      break;
-    }
-    if ((++it & 63) == 0 && (it > SPIN_LIMIT || err_set(p.err))) {
-      if (lane == 0 && it > SPIN_LIMIT) raise_err(p.err, err_code(W_SLIST, 0));
-      return false;
-    }
+  float g0;
+  int r0;
+  if (K < 32) {
+    // two lists per register: three merges of list pairs, then the two halves
+    float g[NX / 2];
+    int gr[NX / 2];
+    if (!gather_slists<NX / 2>(ncu, p, K, tS2, g, gr)) return false;
+    merge32_desc<false>(g[0], gr[0], g[1], gr[1]);
+    merge32_desc<false>(g[2], gr[2], g[3], gr[3]);
+    merge32_desc<false>(g[0], gr[0], g[2], gr[2]);
+    merge32_desc<true>(g[0], gr[0], g[0], gr[0]);
+    g0 = g[0];
+    r0 = gr[0];
+  } else {
+    // a tree of pairwise merges
+    float g[NX];
+    int gr[NX];
+    if (!gather_slists<NX>(ncu, p, K, tS2, g, gr)) return false;
+    merge64_desc(g[0], gr[0], g[1], gr[1]);
+    merge64_desc(g[2], gr[2], g[3], gr[3]);
+    merge64_desc(g[4], gr[4], g[5], gr[5]);
+    merge64_desc(g[6], gr[6], g[7], gr[7]);
+    merge64_desc(g[0], gr[0], g[2], gr[2]);
+    merge64_desc(g[4], gr[4], g[6], gr[6]);
+    merge64_desc(g[0], gr[0], g[4], gr[4]);
+    g0 = g[0];
+    r0 = gr[0];
   }
-  // the 64 largest of the 8 lists, largest first: a tree of pairwise merges
-  merge64_desc(g[0], gr[0], g[1], gr[1]);
-  merge64_desc(g[2], gr[2], g[3], gr[3]);
-  merge64_desc(g[4], gr[4], g[5], gr[5]);
-  merge64_desc(g[6], gr[6], g[7], gr[7]);
-  merge64_desc(g[0], gr[0], g[2], gr[2]);
-  merge64_desc(g[4], gr[4], g[6], gr[6]);
-  merge64_desc(g[0], gr[0], g[4], gr[4]);
-  if (__builtin_amdgcn_readlane(__float_as_int(g[0]), K) == __builtin_amdgcn_readlane(__float_as_int(g[0]), K - 1)) {
+  if (__builtin_amdgcn_readlane(__float_as_int(g0), K) == __builtin_amdgcn_readlane(__float_as_int(g0), K - 1)) {
     // values tie at the k-th largest: the reference keeps them all
     if (lane == 0) raise_err(p.err, err_code(W_SAMPLE, 0));
     return false;
   }
   // the kept values in row order (Sampler.cs:52-68 walks the rows in index order:
   // the exps summed one by one, the first row past u)
-  const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g[0]), 0));
-  int rs = lane < K ? gr[0] : 0x7fffffff;
-  float ps = lane < K ? g[0] : 0.f;
-  sort64_key_asc(rs, ps);
+  const float mx = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(g0), 0));
+  int rs = lane < K ? r0 : 0x7fffffff;
+  float ps = lane < K ? g0 : 0.f;
+  if (K < 32)
+    sort_key_asc<32>(rs, ps);
+  else
+    sort_key_asc<64>(rs, ps);
   const float ex = lane < K ? expf(ps - mx) : 0.f;
-  float acc = 0.f, pre = 0.f;
-  for (int j = 0; j < K; j++) {
-    acc = acc + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), j));
-    if (lane == j) pre = acc;
-  }
+  const float pre = K < 32 ? seq_prefix<32>(ex) : seq_prefix<64>(ex);  // the running sum after row j
+  const float acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pre), K - 1));
   const float u = (float)u01 * acc;
   const uint64_t hit = __ballot(lane < K && u < pre);
   id = hit ? __builtin_amdgcn_readlane(rs, (int)__builtin_ctzll(hit)) : p.V - 1;
@@ -1918,6 +2000,21 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
   trace_mark(p.trace, 31);
 }
 
+#ifdef FH_DECODE_SAMPLED_TU
+}  // namespace
+// decode_fast_sampled.hip compiles this file for the sampled kernel alone: the
+// instantiation and the two entry points the host code below calls.
+hipError_t decode_sampled_occupancy(int* occ) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, k_decode_step<768, 12, true>, NT, 0);
+}
+hipError_t decode_sampled_launch(hipStream_t st, const void* kparams) {
+  hipLaunchKernelGGL((k_decode_step<768, 12, true>), dim3(NB), dim3(NT), 0, st,
+                     *static_cast<const KParams*>(kparams));
+  return hipGetLastError();
+}
+}  // namespace fh
+#else
+
 __global__ void k_xcc_probe(unsigned* out) {
   if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
 }
@@ -2070,8 +2167,12 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   int occ = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH, false>, NT, 0) != hipSuccess || occ < 1)
     return FH_OK;
+  // This file keeps an instantiation of the sampled kernel as well (checked here,
+  // launched from decode_fast_sampled.hip's copy): the greedy kernel's code
+  // generation depends on it (compiled without it, the greedy kernel measured
+  // 152.9 instead of 147.1 us per token).
   sampled_ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH, true>, NT, 0) == hipSuccess &&
-               occ >= 1;
+               occ >= 1 && decode_sampled_occupancy(&occ) == hipSuccess && occ >= 1;
   if (hipGetDevice(&device) != hipSuccess) return FH_ERR_HIP;
   {
     // the XCD-local hand-offs need 8 XCDs dealt blocks round-robin (blocks
@@ -2231,10 +2332,9 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.penalty = s.penalty;
   k.top_k = s.top_k;
   k.ngram = s.ngram;
-  if (s.sampled)
-    hipLaunchKernelGGL((k_decode_step<kD, kH, true>), dim3(NB), dim3(NT), 0, st, k);
-  else
-    hipLaunchKernelGGL((k_decode_step<kD, kH, false>), dim3(NB), dim3(NT), 0, st, k);
+  static_assert(kD == 768 && kH == 12, "the sampled kernel's instantiation");
+  if (s.sampled) return decode_sampled_launch(st, &k) == hipSuccess ? FH_OK : FH_ERR_HIP;
+  hipLaunchKernelGGL((k_decode_step<kD, kH, false>), dim3(NB), dim3(NT), 0, st, k);
   return hipGetLastError() == hipSuccess ? FH_OK : FH_ERR_HIP;
 }
 
@@ -2306,3 +2406,4 @@ void FastDecode::release() {
 }
 
 }  // namespace fh
+#endif  // FH_DECODE_SAMPLED_TU

@@ -6,6 +6,12 @@
 
 namespace fh {
 
+// The sampled persistent kernel (decode_fast_sampled.hip, a translation unit of
+// its own): its occupancy, and a launch of 256 blocks with the kernel's
+// parameter block (`kparams` points at it; it is copied at the launch).
+hipError_t decode_sampled_occupancy(int* occ);
+hipError_t decode_sampled_launch(hipStream_t st, const void* kparams);
+
 // Device state of the persistent decode path for one session.  It runs one
 // batch-1 fp32 decode step per launch: all layers, the tied head and (in
 // greedy mode) the argmax, with dataflow hand-offs between phases.  Sessions
