@@ -20,6 +20,8 @@
 // The blocks are dispatched to the 8 XCDs in turn; the tile order gives each
 // XCD a contiguous run of row-major tiles, so the A rows a run shares are
 // fetched into one L2.
+#include <type_traits>
+
 #include "kernels.hpp"
 #include "mfma_epi.hpp"
 
@@ -217,6 +219,252 @@ __global__ __launch_bounds__(256, 2) void k_gemm_bf16(const bf16_t* __restrict__
   }
 }
 
+// ---- 8-wave ping-pong kernel for windows of many rows -------------------------
+//
+// A block of 8 waves computes BM x 256 tiles (BM 256 or 128), one CU each,
+// looping over the tiles of its XCD's run.  The waves form two groups of four
+// (each SIMD holds one wave of each): group g owns rows [g BM/2, (g+1) BM/2) of
+// the tile, wave q of a group columns [64 q, 64 q + 64).  The groups alternate
+// between two phases separated by barriers: while one multiplies a 32-k step
+// from fragments already in its registers (16 MFMAs, nothing else), the other
+// reads its fragments of the next step from LDS and issues direct-to-LDS loads
+// of the operands two steps ahead, so each SIMD's matrix unit always has one
+// wave feeding it.  K steps rotate through four LDS stages (A rows, then W rows,
+// 64-byte rows with the chunks XOR-swizzled as above).  The products are formed
+// as (W a^T) tiles, W fragment first: a lane then holds 4 consecutive columns of
+// one row, so the epilogue stores 16-byte (fp32) or 8-byte (bf16) pieces.  The
+// accumulation order per output equals k_gemm_bf16's (16-k MFMA steps in k
+// order), so both kernels give the same bits.
+constexpr int PBN = 256;  // columns per tile
+constexpr int PNB = 4;    // LDS stages
+
+// The lane index as a value the compiler cannot move out of a loop: the
+// epilogue's per-lane addresses are then formed where they are used instead of
+// being held in registers through the whole tile loop.
+__device__ __forceinline__ int opaque_lane() {
+  int l;
+  asm volatile("v_and_b32 %0, 63, %1" : "=v"(l) : "v"((int)threadIdx.x));
+  return l;
+}
+
+// a barrier nothing is scheduled across; VM >= 0 first waits until at most VM of
+// this wave's vector memory operations are in flight
+template <int VM>
+__device__ __forceinline__ void pp_sync() {
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (VM == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (VM == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+  if constexpr (VM == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BM, int EPI, bool OUT_BF16>
+__global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restrict__ A, int M, int K,
+                                                        const bf16_t* __restrict__ Wt, int N,
+                                                        const float* __restrict__ bias, GemmBf16Out o, int gm,
+                                                        int gn) {
+  constexpr int MT = BM / 64;              // 32-row accumulator tiles per wave
+  constexpr int NI = (BM + PBN) / 16;      // direct-to-LDS loads (16 rows each) per K step
+  constexpr int NW = NI / 8;               // of them per wave
+  static_assert(NI % 8 == 0 && (NW == 3 || NW == 4), "load split");
+  __shared__ __align__(16) bf16_t S[PNB][BM + PBN][TK];
+  __shared__ __align__(16) float bias_s[PBN];  // the tile's bias, staged at its start
+  const int ntiles = gm * gn, bid = blockIdx.x, nb = gridDim.x;
+  // XCD x = bid % 8 takes the tiles of the run [x T/8, (x+1) T/8) when 8 divides T and the grid
+  const bool runs = ntiles % 8 == 0 && nb % 8 == 0;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = w >> 2, q = w & 3;
+  const int fr = lane & 31, fh = lane >> 5;
+  const int lrow = lane >> 2, lpos = lane & 3;  // a load's lane i fills row i / 4, position i % 4
+  const int nk = K / TK;
+  for (int it = 0;; it++) {
+    const int tt = runs ? bid / 8 + it * (nb / 8) : bid + it * nb;
+    if (tt >= (runs ? ntiles / 8 : ntiles)) break;
+    const int t = runs ? (bid % 8) * (ntiles / 8) + tt : tt;
+    const int m0 = (t / gn) * BM, n0 = (t % gn) * PBN;
+    const int arows = min(BM, M - m0), brows = min(PBN, N - n0);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(A + (size_t)m0 * K), (short)0, arows * K * 2, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(Wt + (size_t)n0 * K), (short)0, brows * K * 2, 0x00020000);
+    // load ii of a K step fills LDS rows [16 ii, 16 ii + 16) (A rows, then W rows);
+    // group g issues [g NI/2, (g+1) NI/2), wave q NW of them.  Steps past the last
+    // re-read it into a stage nobody reads again (no branches around loads).
+    auto dma = [&](int kt) {
+      const int buf = kt % PNB, k0 = min(kt, nk - 1) * TK;
+#pragma unroll
+      for (int j = 0; j < NW; j++) {
+        const int ii = g * (NI / 2) + q * NW + j;
+        const bool isA = ii < BM / 16;
+        const int row = (isA ? 16 * ii : 16 * ii - BM) + lrow;
+        const int c = lpos ^ ((row >> 2) & 3);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(isA ? ra : rb,
+                                                 (__attribute__((address_space(3))) void*)&S[buf][16 * ii][0], 16,
+                                                 (row * K + k0 + 8 * c) * 2, 0, 0, 0);
+      }
+    };
+    f32x16_t acc[2][MT];  // [column tile][row tile]: accumulator rows are columns of y, lanes rows of y
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][i][r] = 0.f;
+    bf16x8_t af[2][MT], bw[2][2];
+    auto frags = [&](int kt) {
+      const int buf = kt % PNB;
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+          af[kk][i] =
+              *reinterpret_cast<const bf16x8_t*>(&S[buf][g * (BM / 2) + i * 32 + fr][8 * swz(fr, 2 * kk + fh)]);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          bw[kk][j] = *reinterpret_cast<const bf16x8_t*>(&S[buf][BM + q * 64 + j * 32 + fr][8 * swz(fr, 2 * kk + fh)]);
+      }
+    };
+    auto mfma = [&]() {
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int i = 0; i < MT; i++)
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bw[kk][j], af[kk][i], acc[j][i], 0, 0, 0);
+    };
+    // K steps 0 and 1 (group 0 loads the A rows, group 1 the W rows of each), and
+    // the bias into LDS: the epilogue then issues no load between its stores
+    dma(0);
+    dma(1);
+    if (tid < PBN) {
+      const float bv = (bias && n0 + tid < N) ? bias[n0 + tid] : 0.f;
+      bias_s[tid] = bv;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    pp_sync<0>();
+    // Step u: group 0 reads its fragments of u and loads u + 2 (phase 2u - 1), then
+    // multiplies u (phase 2u); group 1 multiplies u - 1 (phase 2u - 1), then reads
+    // and loads (phase 2u).  Stage u % 4 is read in phases 2u - 1 and 2u and
+    // refilled (step u + 4) from phase 2u + 3 on; each wave's loads of step u + 1
+    // have landed (vmcnt) before the barrier that opens phase 2u + 1.
+    if (g == 0) {
+      for (int u = 0; u < nk; u++) {
+        frags(u);
+        dma(u + 2);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        pp_sync<-1>();
+        mfma();
+        pp_sync<NW>();
+      }
+    } else {
+      for (int u = 0; u < nk; u++) {
+        if (u > 0) mfma();
+        pp_sync<-1>();
+        frags(u);
+        dma(u + 2);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        pp_sync<NW>();
+      }
+      mfma();
+    }
+    // epilogue: lane (fr, fh), register 4 a + b of acc[j][i] is column
+    // n0 + 64 q + 32 j + 8 a + 4 fh + b of row m0 + BM/2 g + 32 i + fr.  Each
+    // 32-row chunk i of a wave goes through LDS (bias and GELU applied, rounded
+    // for bf16 outputs), in 16-byte units XOR-swizzled by row, and leaves as
+    // whole row pieces: 16 lanes x 16 bytes per fp32 row of 64 columns, 8 per
+    // bf16 row.  Rows past M and columns past N are dropped by the buffer bounds
+    // (offsets past them), not branches; no load sits between the stores (loads
+    // and stores share one completion counter).
+    pp_sync<0>();  // the last loads have landed and every wave is past its fragment reads
+    const int el = opaque_lane(), efr = el & 31, efh = el >> 5;
+    int pos0 = 0, D = 0, part = 0;
+    if constexpr (EPI == EPI_QKV) {
+      D = N / 3;
+      pos0 = o.src.pos_off + o.src.pos_mul * *o.src.step;
+      part = (n0 + q * 64) / D;  // the wave's 64 columns lie in one of q, K, V (64 | D)
+    }
+    const int mrows = min(BM, M - m0);
+    constexpr int YE = OUT_BF16 ? 2 : 4;
+    const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+        OUT_BF16 ? static_cast<void*>(o.yh + (size_t)m0 * N) : static_cast<void*>(o.y + (size_t)m0 * N), (short)0,
+        EPI == EPI_QKV ? 0 : mrows * N * YE, 0x00020000);
+    char* stg = reinterpret_cast<char*>(&S[0][0][0]) + w * 8192;  // 32 rows x 256 bytes per wave
+    // read-back role of lane l: fp32 rows 4 k + l / 16 (k < 8), unit l % 16 (4 columns);
+    // bf16 rows 8 k + l / 8 (k < 4), unit l % 8 (8 columns).  A buffer's range
+    // check covers the vector offset only, so the whole offset goes there: the
+    // lane's row and columns, or 2^31 (past every bound: the host keeps a tile's
+    // rows under 2^31 bytes) when its columns lie past N.
+    constexpr int RK = OUT_BF16 ? 4 : 8, RS = OUT_BF16 ? 8 : 4;
+    const int ru = OUT_BF16 ? (el & 7) : (el & 15), rrow0 = OUT_BF16 ? (el >> 3) : (el >> 4);
+    const int gcol = n0 + q * 64 + (OUT_BF16 ? 8 : 4) * ru;  // first column of the lane's piece
+    auto eoff = [&](int i, int k, int esz) {
+      const int lr = g * (BM / 2) + i * 32 + RS * k + rrow0;  // row within the tile
+      return gcol < N ? (unsigned)((lr * N + gcol) * esz) : 0x80000000u;
+    };
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+      // 1. this chunk into the wave's staging rows
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+          const float4 bc = *reinterpret_cast<const float4*>(&bias_s[q * 64 + j * 32 + 8 * a + 4 * efh]);
+          const float bcv[4] = {bc.x, bc.y, bc.z, bc.w};
+          float v[4];
+#pragma unroll
+          for (int b = 0; b < 4; b++) {
+            v[b] = acc[j][i][4 * a + b] + bcv[b];
+            if constexpr (EPI == EPI_GELU) v[b] = OUT_BF16 ? gelu_for_bf16(v[b]) : gelu_tanh(v[b]);
+          }
+          if constexpr (OUT_BF16) {
+            typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+            const u32x2_t pk = {(unsigned)__builtin_bit_cast(unsigned short, bf16_rn(v[0])) |
+                                    ((unsigned)__builtin_bit_cast(unsigned short, bf16_rn(v[1])) << 16),
+                                (unsigned)__builtin_bit_cast(unsigned short, bf16_rn(v[2])) |
+                                    ((unsigned)__builtin_bit_cast(unsigned short, bf16_rn(v[3])) << 16)};
+            const int u = (4 * j + a) ^ (efr & 7);  // 16-byte unit of the 128-byte row, half fh
+            *reinterpret_cast<u32x2_t*>(stg + efr * 128 + u * 16 + efh * 8) = pk;
+          } else {
+            const int u = (8 * j + 2 * a + efh) ^ (efr & 15);
+            *reinterpret_cast<float4*>(stg + efr * 256 + u * 16) = make_float4(v[0], v[1], v[2], v[3]);
+          }
+        }
+      // 2. whole row pieces out (the wave's LDS operations complete in order)
+#pragma unroll
+      for (int k = 0; k < RK; k++) {
+        const int cr = rrow0 + RS * k;  // row within the chunk
+        const int row = m0 + g * (BM / 2) + i * 32 + cr;
+        if constexpr (OUT_BF16) {
+          const u32x4_t x = *reinterpret_cast<const u32x4_t*>(stg + cr * 128 + ((ru ^ (cr & 7)) * 16));
+          if constexpr (EPI == EPI_QKV) {
+            const int e = gcol - part * D;
+            if (row < M && gcol < N) {
+              if (part == 0) {
+                *reinterpret_cast<u32x4_t*>(o.q + (size_t)row * D + e) = x;
+              } else {
+                const int bb = row / o.T, pos = pos0 + (row - bb * o.T);
+                bf16_t* cache = part == 1 ? o.kc : o.vc;
+                if ((unsigned)pos < (unsigned)o.ctx)
+                  *reinterpret_cast<u32x4_t*>(cache + (((size_t)bb * o.H + (e >> 6)) * o.ctx + pos) * 64 +
+                                              (e & 63)) = x;
+              }
+            }
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b128(x, ry, eoff(i, k, 2), 0, 0);
+          }
+        } else {
+          const u32x4_t x = *reinterpret_cast<const u32x4_t*>(stg + cr * 256 + ((ru ^ (cr & 15)) * 16));
+          __builtin_amdgcn_raw_buffer_store_b128(x, ry, eoff(i, k, 4), 0, 0);
+        }
+      }
+    }
+    // every wave is past its LDS reads and stores before the next tile's loads
+    pp_sync<0>();
+  }
+}
+
 }  // namespace
 
 template <int BM, int EPI, bool RES, bool OUT_BF16>
@@ -239,6 +487,39 @@ static hipError_t launch_bm(hipStream_t st, int gm, int gn, const bf16_t* a, int
   return hipErrorInvalidValue;  // an epilogue combination no caller uses
 }
 
+template <int BM, int EPI, bool OUT_BF16>
+static hipError_t launch_pp_tiles(hipStream_t st, int gm, int gn, int nb, const bf16_t* a, int M, int K,
+                                  const bf16_t* Wt, int N, const float* bias, const GemmBf16Out& o) {
+  hipLaunchKernelGGL((k_gemm_bf16_pp<BM, EPI, OUT_BF16>), dim3(nb), dim3(512), 0, st, a, M, K, Wt, N, bias, o, gm,
+                     gn);
+  return hipGetLastError();
+}
+
+// one block per CU (rounded down to a multiple of 8, the XCD count), at most one per tile
+static int pp_blocks(int ntiles) {
+  static const int cus = [] {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                hipSuccess || v < 8)
+      return 8;
+    return v / 8 * 8;
+  }();
+  return ntiles < cus ? ntiles : cus;
+}
+
+template <int BM>
+static hipError_t launch_pp(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
+                            const float* bias, int epi, const GemmBf16Out& o) {
+  const int gm = (M + BM - 1) / BM, gn = (N + PBN - 1) / PBN, nb = pp_blocks(gm * gn);
+  const bool gelu = epi == EPI_GELU;
+  if (o.res) return hipErrorInvalidValue;  // residual GEMMs take k_gemm_bf16
+  if (epi == EPI_QKV) return launch_pp_tiles<BM, EPI_QKV, true>(st, gm, gn, nb, a, M, K, Wt, N, bias, o);
+  if (!gelu && o.y) return launch_pp_tiles<BM, EPI_NONE, false>(st, gm, gn, nb, a, M, K, Wt, N, bias, o);
+  if (gelu && o.yh) return launch_pp_tiles<BM, EPI_GELU, true>(st, gm, gn, nb, a, M, K, Wt, N, bias, o);
+  if (gelu && o.y) return launch_pp_tiles<BM, EPI_GELU, false>(st, gm, gn, nb, a, M, K, Wt, N, bias, o);
+  return hipErrorInvalidValue;  // an epilogue combination no caller uses
+}
+
 static hipError_t launch_any(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
                              const float* bias, int epi, const GemmBf16Out& o) {
   // bf16 outputs leave as 16-byte pieces of 8 columns
@@ -246,6 +527,20 @@ static hipError_t launch_any(hipStream_t st, const bf16_t* a, int M, int K, cons
     return hipErrorInvalidValue;
   // byte offsets inside a block's rows (operands and outputs) are 32-bit
   if ((size_t)256 * K * 2 > 0x7fffffffu || (size_t)256 * N * 4 > 0x7fffffffu) return hipErrorInvalidValue;
+  // The ping-pong kernel without a residual once 256-row tiles give one per CU,
+  // or 128-row tiles one per two CUs (C5: qkv and mlp.fc on 256-row tiles; the
+  // residual GEMMs attn.proj and mlp.proj measured no faster on it, 32.2 / 90.1
+  // against 30.9 / 90.8 us, and stay below); its stores need 16-byte aligned
+  // fp32 rows and 8-byte aligned bf16 ones.
+  {
+    auto al = [](const void* p, unsigned n) { return ((uintptr_t)p & (n - 1)) == 0; };
+    const bool pp_ok = !o.res && N % 4 == 0 && al(o.y, 16) && al(o.yh, 8) && al(o.q, 8) && al(o.kc, 8) && al(o.vc, 8);
+    const int pn = (N + PBN - 1) / PBN;
+    if (pp_ok && ((M + 255) / 256) * pn >= pp_blocks(1 << 30))
+      return launch_pp<256>(st, a, M, K, Wt, N, bias, epi, o);
+    if (pp_ok && ((M + 127) / 128) * pn >= pp_blocks(1 << 30) / 2)
+      return launch_pp<128>(st, a, M, K, Wt, N, bias, epi, o);
+  }
   const int gn = (N + TN - 1) / TN;
   // 256-row tiles while they give two tiles per CU (two blocks fit a CU); 128 below
   // that (attn.proj and mlp.proj at N 1024: 512 tiles of 128 rows instead of 256

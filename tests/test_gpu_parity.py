@@ -468,6 +468,32 @@ def test_matmul_nn_bf16_large_tiles(fhp, backend, M, K, N):
         buf.free()
 
 
+@pytest.mark.parametrize("M,K,N", [(2000, 512, 4000), (4100, 1024, 4100), (8192, 1024, 3072)])
+def test_matmul_nn_bf16_pingpong_tiles(fhp, backend, M, K, N):
+    # bf16 products without accumulation over many rows run on the 8-wave
+    # ping-pong kernel: 128-row tiles (first case, ragged in M and N: rows and
+    # columns past the ends dropped by the store bounds), 256-row tiles looping
+    # over several tiles per block (second case ragged, third the C5 qkv shape)
+    r = np.random.default_rng(M + K + N + 1)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    a_used, _ = bf16_round(a)
+    b_used, b_bits = bf16_round(b)
+    bufa = fhp.DeviceBuffer.from_array(backend, a)
+    bufb = fhp.DeviceBuffer.from_array(backend, b_bits)
+    # a sentinel past the last row checks that nothing is stored beyond the output
+    bufy = fhp.DeviceBuffer.from_array(backend, np.full((M + 64, N), 7.0, np.float32))
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=False, dtype="bf16")
+    full = bufy.read(np.float32, (M + 64) * N).reshape(M + 64, N)
+    got = full[:M]
+    ref = a_used.astype(np.float64) @ b_used.astype(np.float64)
+    scale = np.abs(a_used).astype(np.float64) @ np.abs(b_used).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= 1e-5 * scale + 1e-6), float(np.max(np.abs(got - ref) / (scale + 1e-6)))
+    assert np.all(full[M:] == 7.0)
+    for buf in (bufa, bufb, bufy):
+        buf.free()
+
+
 def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
     # Forge-220M shape with bf16 weights, reduced to a 64-token
     # prompt and 3 steps per sequence so the CPU oracle stays quick; the oracle runs
