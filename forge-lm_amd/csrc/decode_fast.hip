@@ -572,11 +572,12 @@ struct SampLds<true> {
 // ROWS of them stay in LDS for the whole launch (the table does not change
 // between steps, so they are read from HBM once per launch instead of once per
 // token; 12 fill the LDS the sampled kernel leaves); INFLIGHT of the rest stream
-// from HBM at a time.  Both are measured per kernel: the greedy kernel streams
-// every row three at a time (holding rows in LDS shortened its head but slowed
-// its layers by more), the sampled kernel holds 12 and streams two at a time.
+// from HBM at a time.  Both are measured per kernel: the greedy kernel holds 4
+// and streams three at a time (145.7 against 147.5 us per token holding none; 6,
+// 8 or 12 rows measured 152.7-156.7: the layers' code came out slower), the
+// sampled kernel holds 12 and streams two at a time.
 #ifndef FH_HRES_G
-#define FH_HRES_G 0
+#define FH_HRES_G 4
 #endif
 #ifndef FH_HRES_S
 #define FH_HRES_S 12
