@@ -188,23 +188,26 @@ def copy_calibration(mib: int, reps: int) -> dict:
 
 
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_step_c2_traffic.md")
+TRAFFIC_PROFILE_2 = os.path.join("profiles", "traffic_c3_c4_c5.md")
 
 
-def profiled_traffic(kernel: str):
-    """(HBM bytes per launch of `kernel`, what build they were counted on) from the
-    committed counter summary (two rocprofv3 --pmc runs; the counters cannot be read
-    inside this run), or (None, None)."""
-    value, build = None, None
+def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
+    """(HBM bytes per launch of `kernel`, HBM / algorithmic bytes of `kernel`, what
+    build they were counted on) from a committed counter summary (rocprofv3 --pmc
+    runs; the counters cannot be read inside this run); None where it has none."""
+    value, ratio, build = None, None, None
     try:
-        with open(os.path.join(ROOT, TRAFFIC_PROFILE)) as f:
+        with open(os.path.join(ROOT, path)) as f:
             for line in f:
                 if line.startswith("traffic_bytes_per_launch:") and kernel in line:
                     value = int(line.split(":", 1)[1].split()[0])
+                elif line.startswith("traffic_ratio:") and kernel in line:
+                    ratio = float(line.split(":", 1)[1].split()[0])
                 elif line.startswith("measured_on:"):
                     build = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return value, build
+    return value, ratio, build
 
 
 def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: int = 0) -> dict:
@@ -258,6 +261,7 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
         "config": {"workload": w["desc"], "batch": B, "prompt_len": P, "new_tokens": NEW},
     }
     if name == "c5":
+        c5_traffic, _, c5_build = profiled_traffic("prefill forward", TRAFFIC_PROFILE_2)
         flops = prefill_flops(c, min(P, ctx), B)
         tflops = flops / pre_s / 1e12
         pre_tok = B * min(P, ctx) / pre_s
@@ -269,10 +273,12 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
             "reprefill_ms_per_step": round(avg_step_s * 1e3, 3),
             "whole_job_tok_s": round(value, 2),
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
-                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                         "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": c5_traffic,
                          "kernel": "prefill forward (GEMM, attention, LayerNorm, head kernels)",
                          "flops_per_launch": flops, "launch_us": round(pre_s * 1e6, 1)},
         })
+        if c5_traffic is not None:
+            out["roofline"]["traffic_source"] = f"{TRAFFIC_PROFILE_2} (counted on {c5_build})"
         # the timed unit is one prefill forward; value is its token rate
         out["steps"] = steps
     else:
@@ -291,7 +297,20 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
         else:
             kernel = "decode step graph (generic kernels)"
         tokens_per_launch = n_dec if persistent else 1
-        traffic, traffic_build = profiled_traffic(kernel) if (persistent and name == "c2") else (None, None)
+        traffic, traffic_src = None, None
+        if persistent and name == "c2":
+            traffic, _, build = profiled_traffic(kernel)
+            traffic_src = f"{TRAFFIC_PROFILE} (counted on {build})" if traffic is not None else None
+        elif persistent and name == "c3":
+            traffic, _, build = profiled_traffic(kernel, TRAFFIC_PROFILE_2)
+            traffic_src = f"{TRAFFIC_PROFILE_2} (counted on {build})" if traffic is not None else None
+        elif not persistent and name == "c4":
+            _, ratio, build = profiled_traffic(kernel, TRAFFIC_PROFILE_2)
+            if ratio is not None:
+                # the counted HBM / algorithmic ratio applied to this run's windows
+                traffic = int(ratio * step_bytes * tokens_per_launch)
+                traffic_src = (f"{TRAFFIC_PROFILE_2}: HBM / algorithmic bytes {ratio:.4f} counted at windows "
+                               f"513..576 ({build}), times this run's algorithmic bytes")
         out.update({
             "decode_tok_s": round(B * n_dec / dec_s, 2),
             "decode_us_per_step": round(avg_step_s * 1e6, 2),
@@ -304,7 +323,7 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
                          "launch_us": round(avg_step_s * tokens_per_launch * 1e6, 2)},
         })
         if traffic is not None:
-            out["roofline"]["traffic_source"] = f"{TRAFFIC_PROFILE} (counted on {traffic_build})"
+            out["roofline"]["traffic_source"] = traffic_src
         if name == "c2":
             out["metric"] = "decode tok/s, Forge-98M shape fp32 bs1 (prompt 64 + 256 greedy)"
             out["decode_us_per_token"] = out.pop("decode_us_per_step")
