@@ -35,6 +35,30 @@ __device__ __forceinline__ int acc_row(int lane, int r) { return (r >> 2) * 8 + 
 
 __device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__bf16, bf16_rn(f)); }
 
+// Block -> (query block, head, sequence) of a causal prefill launched as one
+// grid dimension of nqb * H * B blocks; query block 0 holds the last BQ
+// queries (the most keys).  Workgroups reach the 8 XCDs round-robin by linear
+// index, so a grid ordered by query block gives one XCD every heaviest block.
+// When nqb is even and 8 divides H * B, XCD x takes whole (sequence, head)
+// groups (their K/V rows are fetched into its L2 once) as pairs of query
+// blocks i and nqb - 1 - i, whose costs add to the same total.  A block's
+// partner is the next index on its XCD, and the order within pairs flips every
+// 32 indices, so 4 blocks a CU receives, consecutive on the XCD or 32 apart,
+// form two whole pairs.  Otherwise the blocks keep the heaviest-first order.
+struct QBlock {
+  int qb, h, b;
+};
+__device__ __forceinline__ QBlock prefill_block(int L, int nqb, int H) {
+  const int G = gridDim.x / nqb;  // H * B
+  if ((nqb & 1) == 0 && G % 8 == 0) {
+    const int xcd = L & 7, s = L >> 3, j = s >> 1, half = nqb >> 1;
+    const int xh = j % half, g = xcd * (G / 8) + j / half;
+    const bool light = ((s + (s >> 5)) & 1) != 0;
+    return {light ? nqb - 1 - xh : xh, g % H, g / H};
+  }
+  return {L % nqb, (L / nqb) % H, L / (nqb * H)};
+}
+
 template <typename KT, typename OT, typename QT>
 __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict__ qp, int qstride, int T, int d, int H,
                                                           int ctx, const KT* __restrict__ kc,
@@ -48,7 +72,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
   __shared__ __align__(16) E Vt[HD][BKV + PAD];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int t0 = blockIdx.x * BQ, h = blockIdx.y, b = blockIdx.z;
+  const int nqb = (T + BQ - 1) / BQ;
+  const QBlock qbk = prefill_block(blockIdx.x, nqb, H);
+  const int t0 = (nqb - 1 - qbk.qb) * BQ, h = qbk.h, b = qbk.b;
   const int qw0 = t0 + 32 * w;             // this wave's first query
   const int q = qw0 + (lane & 31), half = lane >> 5;
   const float scale = 0.125f;              // 1 / sqrt(64), exact
@@ -254,7 +280,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
 // log2(e) / 8), the causal mask only on tiles that cross the wave's diagonal,
 // and P is rounded to bf16 by the hardware packed convert.  Rows at or past T
 // read as zeros (bounded buffer loads), so stale cache rows never meet a zero
-// weight.  The heaviest query blocks (latest queries) are dispatched first.
+// weight.  Blocks take query blocks in prefill_block's XCD-balanced order.
 // ---------------------------------------------------------------------------
 constexpr int KP = HD + 8;  // bf16 per LDS row of K (dims) and V^T (keys): 144 B, 16 rows hit distinct banks
 
@@ -265,7 +291,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __re
   __shared__ __align__(16) __bf16 Vt[2][HD][KP];
 
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int t0 = (gridDim.x - 1 - blockIdx.x) * BQ, h = blockIdx.y, b = blockIdx.z;
+  const int nqb = (T + BQ - 1) / BQ;
+  const QBlock qbk = prefill_block(blockIdx.x, nqb, H);
+  const int t0 = (nqb - 1 - qbk.qb) * BQ, h = qbk.h, b = qbk.b;
   const int qw0 = t0 + 32 * w;
   const int q = qw0 + (lane & 31), half = lane >> 5;
   const float sl2 = 0.125f * 1.4426950408889634f;  // 1/sqrt(64) * log2(e)
@@ -425,7 +453,7 @@ hipError_t launch_attn_prefill_mfma(hipStream_t st, const float* qkv, int B, int
   if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !qkv || !kcache || !vcache || !o ||
       (size_t)T * HD * sizeof(KT) > 0x7fffffffu)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL((k_attn_prefill_mfma<KT, OT, float>), dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, qkv,
+  hipLaunchKernelGGL((k_attn_prefill_mfma<KT, OT, float>), dim3((T + BQ - 1) / BQ * H * B), dim3(256), 0, st, qkv,
                      3 * d, T, d, H, ctx, kcache, vcache, o);
   return hipGetLastError();
 }
@@ -435,7 +463,7 @@ hipError_t launch_attn_prefill_mfma_q16(hipStream_t st, const bf16_t* q, int B, 
   if (B <= 0 || T <= 0 || T > ctx || H <= 0 || d != H * HD || !q || !kcache || !vcache || !o)
     return hipErrorInvalidValue;
   if ((size_t)T * HD * 2 > 0x7fffffffu) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_prefill_bf16, dim3((T + BQ - 1) / BQ, H, B), dim3(256), 0, st, q, T, d, H, ctx, kcache,
+  hipLaunchKernelGGL(k_attn_prefill_bf16, dim3((T + BQ - 1) / BQ * H * B), dim3(256), 0, st, q, T, d, H, ctx, kcache,
                      vcache, o);
   return hipGetLastError();
 }
