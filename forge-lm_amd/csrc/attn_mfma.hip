@@ -276,8 +276,8 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
 // and packs them with v_perm into two 16-byte rows of V^T.  Within each group
 // of 16 keys V^T holds the keys in the order the score registers hold them
 // (0-3, 8-11, 4-7, 12-15), so an A fragment is one 16-byte LDS read.  The
-// softmax runs in base 2 on the hardware exp (scores pre-scaled by
-// log2(e) / 8), the causal mask only on tiles that cross the wave's diagonal,
+// softmax runs in base 2 on the hardware exp (the scale log2(e) / 8 folded into
+// one FMA per score), the causal mask only on tiles that cross the wave's diagonal,
 // and P is rounded to bf16 by the hardware packed convert.  Rows at or past T
 // read as zeros (bounded buffer loads), so stale cache rows never meet a zero
 // weight.  Blocks take query blocks in prefill_block's XCD-balanced order.
@@ -369,6 +369,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __re
           s[jt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qb[kk], s[jt], 0, 0, 0);
         }
       }
+      // the maximum is taken on the raw products (the scale is positive) and the
+      // scale folded into the exponent: p = 2^(s * log2(e) / 8 - m)
       float mt = -INFINITY;
       if (k0 + BKV - 1 > qw0) {  // the tile crosses this wave's diagonal: mask keys past the query
 #pragma unroll
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __re
 #pragma unroll
           for (int r = 0; r < 16; r++) {
             const int key = k0 + jt * 32 + acc_row(lane, r);
-            const float v = key <= q ? s[jt][r] * sl2 : -INFINITY;
+            const float v = key <= q ? s[jt][r] : -INFINITY;
             s[jt][r] = v;
             mt = fmaxf(mt, v);
           }
@@ -384,22 +386,19 @@ __global__ __launch_bounds__(256, 2) void k_attn_prefill_bf16(const bf16_t* __re
 #pragma unroll
         for (int jt = 0; jt < 2; jt++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) {
-            s[jt][r] *= sl2;
-            mt = fmaxf(mt, s[jt][r]);
-          }
+          for (int r = 0; r < 16; r++) mt = fmaxf(mt, s[jt][r]);
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mn = fmaxf(m, mt);
       // a lane whose query precedes every key of the tile keeps mn = m; its
       // first tile (key 0) always has a visible key, so mn is finite here
+      const float mn = fmaxf(m, mt * sl2);
       const float corr = __builtin_amdgcn_exp2f(m - mn);
       float ls = 0.f;
 #pragma unroll
       for (int jt = 0; jt < 2; jt++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const float p = __builtin_amdgcn_exp2f(s[jt][r] - mn);
+          const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(s[jt][r], sl2, -mn));
           s[jt][r] = p;
           ls += p;
         }

@@ -236,6 +236,10 @@ struct fh_session {
   float *x = nullptr, *x2 = nullptr, *xn = nullptr, *qkv = nullptr, *o = nullptr, *h = nullptr;
   float *part = nullptr, *apart = nullptr, *logits = nullptr, *work = nullptr;
   size_t part_floats = 0;
+  // bf16 sessions: arrival counters of the window mlp.proj with K split in two
+  // (one per 256 x 256 tile, zero between launches; o holds the first halves' sums)
+  int* gsplit = nullptr;
+  int gsplit_cap = 0;
   int* step = nullptr;
   int* done = nullptr;
   int* out_counts = nullptr;
@@ -408,8 +412,10 @@ int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src) {
     LAUNCH(launch_layernorm_bf16(st, s->x2, M, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), xnh, D, 1e-5f));
     LAUNCH(launch_gemm_bf16(st, xnh, M, D, s->wt<bf16_t>(s->idx_blk(l, 8)), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU,
                             nullptr, nullptr, hh));
-    LAUNCH(launch_gemm_bf16(st, hh, M, 4 * D, s->wt<bf16_t>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)),
-                            EPI_RESIDUAL, s->x2, s->x, nullptr));
+    // mlp.proj: o (the attention output, consumed by attn.proj) holds the sums of
+    // the first K halves when the product is split
+    LAUNCH(launch_gemm_bf16_split(st, hh, M, 4 * D, s->wt<bf16_t>(s->idx_blk(l, 10)), D, s->v(s->idx_blk(l, 11)),
+                                  s->x2, s->x, s->o, (size_t)B * C * D, s->gsplit, s->gsplit_cap));
   }
   return FH_OK;
 }
@@ -925,15 +931,24 @@ int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_de
     // for bf16 with many rows, for a rounded to bf16: the window path's kernel)
     const bool big = bf && M >= 256 && K % 64 == 0;
     const size_t esz = bf ? 2 : 4, part_floats = big ? 0 : (size_t)8 * M * N;
+    // an accumulating bf16 product may split K in two: first halves' sums and tile counters
+    const size_t ws_floats = big && res ? (size_t)M * N : 0;
+    const int ncnt = big && res ? ((M + 255) / 256) * ((N + 255) / 256) : 0;
     char* tmp = nullptr;
-    HIP_TRY(hipMalloc(&tmp, (size_t)N * K * esz + (big ? (size_t)M * K * 2 : part_floats * 4)));
+    const size_t wbytes = (size_t)N * K * esz + (big ? (size_t)M * K * 2 : part_floats * 4);
+    HIP_TRY(hipMalloc(&tmp, (wbytes + 255) / 256 * 256 + ws_floats * 4 + (size_t)ncnt * 4));
     float* part = reinterpret_cast<float*>(tmp + (size_t)N * K * esz);
+    float* ws = reinterpret_cast<float*>(tmp + (wbytes + 255) / 256 * 256);
+    int* cnt = reinterpret_cast<int*>(ws + ws_floats);
     if (big) {
       bf16_t* wt = reinterpret_cast<bf16_t*>(tmp);
       bf16_t* ah = wt + (size_t)N * K;
       e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, wt);
       if (e == hipSuccess) e = launch_round_bf16(st, a, (size_t)M * K, ah);
-      if (e == hipSuccess) e = launch_gemm_bf16(st, ah, M, K, wt, N, nullptr, EPI_NONE, res, y, nullptr);
+      if (e == hipSuccess && res) e = hipMemsetAsync(cnt, 0, (size_t)ncnt * 4, st);
+      if (e == hipSuccess)
+        e = res ? launch_gemm_bf16_split(st, ah, M, K, wt, N, nullptr, res, y, ws, ws_floats, cnt, ncnt)
+                : launch_gemm_bf16(st, ah, M, K, wt, N, nullptr, EPI_NONE, res, y, nullptr);
     } else if (bf) {
       e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, reinterpret_cast<bf16_t*>(tmp));
       if (e == hipSuccess)
@@ -1032,6 +1047,12 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
       (rc = dev_alloc(&sp->work, (size_t)B * V)) || (rc = dev_alloc(&sp->step, 1)) || (rc = dev_alloc(&sp->done, 1)) ||
       (rc = dev_alloc(&sp->out_counts, B)))
     return fail(rc);
+  if (sp->esize == 2) {
+    sp->gsplit_cap = (int)((rows + 255) / 256) * ((D + 255) / 256);
+    if ((rc = dev_alloc(&sp->gsplit, sp->gsplit_cap)) != FH_OK) return fail(rc);
+    const hipError_t he = hipMemset(sp->gsplit, 0, (size_t)sp->gsplit_cap * sizeof(int));
+    if (he != hipSuccess) return fail(set_err(FH_ERR_HIP, "hipMemset: %s", hipGetErrorString(he)));
+  }
   for (auto& e : sp->ev) {
     hipError_t he = hipEventCreate(&e);
     if (he != hipSuccess) return fail(set_err(FH_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(he)));
@@ -1065,7 +1086,7 @@ int fh_session_destroy(fh_session* s) {
   dev_free(vc);
   dev_free(s->x); dev_free(s->x2); dev_free(s->xn); dev_free(s->qkv); dev_free(s->o); dev_free(s->h);
   dev_free(s->part); dev_free(s->apart); dev_free(s->logits); dev_free(s->work);
-  dev_free(s->step); dev_free(s->done); dev_free(s->out_counts);
+  dev_free(s->step); dev_free(s->done); dev_free(s->out_counts); dev_free(s->gsplit);
   dev_free(s->tokens); dev_free(s->out_ids); dev_free(s->uniforms); dev_free(s->dump);
   fh_context* c = s->ctx;
   const bool counted = s->counted;

@@ -259,7 +259,25 @@ __device__ __forceinline__ void pp_sync() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BM, int EPI, bool OUT_BF16>
+// SPLIT (BM 256, fp32 y with the residual): items are (tile, K half) pairs, both
+// halves of a tile in one XCD's run; the first half to finish stores its raw sums
+// in o.ws and marks the tile's counter ready, the second waits for the mark, adds
+// them and runs the epilogue, then clears the counter for the next launch.  The
+// sums pass through the XCD's L2 (plain stores, loads that miss the CU's L1), so
+// both halves must run on one XCD: workgroups reach the XCDs round-robin by index
+// (continuing from the previous dispatch, so blocks b and b + 8 share one), the
+// two halves of a tile are such a pair, each adds its hardware XCD to the tile's
+// counter, and a second half that finds the first on another XCD writes NaN
+// instead of sums it might not see.
+constexpr int SPLIT_READY = 0x10000;
+
+__device__ __forceinline__ int hw_xcc() {
+  unsigned v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return (int)(v & 0xf);
+}
+
+template <int BM, int EPI, bool OUT_BF16, bool SPLIT = false>
 __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restrict__ A, int M, int K,
                                                         const bf16_t* __restrict__ Wt, int N,
                                                         const float* __restrict__ bias, GemmBf16Out o, int gm,
@@ -270,18 +288,21 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
   static_assert(NI % 8 == 0 && (NW == 3 || NW == 4), "load split");
   __shared__ __align__(16) bf16_t S[PNB][BM + PBN][TK];
   __shared__ __align__(16) float bias_s[PBN];  // the tile's bias, staged at its start
-  const int ntiles = gm * gn, bid = blockIdx.x, nb = gridDim.x;
-  // XCD x = bid % 8 takes the tiles of the run [x T/8, (x+1) T/8) when 8 divides T and the grid
+  __shared__ int role_s, ready_s;  // SPLIT: the tile's counter before this half arrived; the mark was seen
+  static_assert(!SPLIT || (BM == 256 && EPI == EPI_NONE && !OUT_BF16), "split: fp32 y with the residual");
+  const int ntiles = SPLIT ? 2 * gm * gn : gm * gn, bid = blockIdx.x, nb = gridDim.x;
+  // XCD x = bid % 8 takes the items of the run [x T/8, (x+1) T/8) when 8 divides T and the grid
   const bool runs = ntiles % 8 == 0 && nb % 8 == 0;
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = w >> 2, q = w & 3;
   const int fr = lane & 31, fh = lane >> 5;
   const int lrow = lane >> 2, lpos = lane & 3;  // a load's lane i fills row i / 4, position i % 4
-  const int nk = K / TK;
+  const int nk = SPLIT ? K / TK / 2 : K / TK;  // K steps per item
   for (int it = 0;; it++) {
     const int tt = runs ? bid / 8 + it * (nb / 8) : bid + it * nb;
     if (tt >= (runs ? ntiles / 8 : ntiles)) break;
-    const int t = runs ? (bid % 8) * (ntiles / 8) + tt : tt;
+    const int item = runs ? (bid % 8) * (ntiles / 8) + tt : tt;
+    const int t = SPLIT ? item >> 1 : item, ks0 = SPLIT ? (item & 1) * nk : 0;  // tile, first K step
     const int m0 = (t / gn) * BM, n0 = (t % gn) * PBN;
     const int arows = min(BM, M - m0), brows = min(PBN, N - n0);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
@@ -292,7 +313,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
     // group g issues [g NI/2, (g+1) NI/2), wave q NW of them.  Steps past the last
     // re-read it into a stage nobody reads again (no branches around loads).
     auto dma = [&](int kt) {
-      const int buf = kt % PNB, k0 = min(kt, nk - 1) * TK;
+      const int buf = kt % PNB, k0 = (ks0 + min(kt, nk - 1)) * TK;
 #pragma unroll
       for (int j = 0; j < NW; j++) {
         const int ii = g * (NI / 2) + q * NW + j;
@@ -378,6 +399,29 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
     // (offsets past them), not branches; no load sits between the stores (loads
     // and stores share one completion counter).
     pp_sync<0>();  // the last loads have landed and every wave is past its fragment reads
+    bool second = false, xok = true;  // SPLIT: this half adds the other's sums and writes y
+    if constexpr (SPLIT) {
+      const int xcc = hw_xcc();
+      if (tid == 0)
+        role_s = __hip_atomic_fetch_add(o.cnt + t, 1 + ((xcc + 1) << 4), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      second = (role_s & 0xf) != 0;
+      xok = !second || ((role_s >> 4) & 0xff) == xcc + 1;  // the first half ran on this XCD
+      if (second) {
+        // the first half has arrived: wait (bounded) until its sums are stored
+        if (tid == 0) {
+          int ok = 0;
+          for (int n = 0; n < (1 << 22) && !ok; n++) {
+            ok = (__hip_atomic_load(o.cnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & SPLIT_READY) != 0;
+            if (!ok) __builtin_amdgcn_s_sleep(2);
+          }
+          ready_s = ok;
+          __hip_atomic_store(o.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
+        }
+        __syncthreads();
+      }
+    }
+    const bool bad = SPLIT && second && (ready_s == 0 || !xok);  // not ready, or not one XCD: y is NaN
     const int el = opaque_lane(), efr = el & 31, efh = el >> 5;
     int pos0 = 0, D = 0, part = 0;
     if constexpr (EPI == EPI_QKV) {
@@ -387,10 +431,20 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
     }
     const int mrows = min(BM, M - m0);
     constexpr int YE = OUT_BF16 ? 2 : 4;
+    // SPLIT: the first half writes its sums to ws, the second y (reading ws and the residual)
     const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-        OUT_BF16 ? static_cast<void*>(o.yh + (size_t)m0 * N) : static_cast<void*>(o.y + (size_t)m0 * N), (short)0,
-        EPI == EPI_QKV ? 0 : mrows * N * YE, 0x00020000);
-    char* stg = reinterpret_cast<char*>(&S[0][0][0]) + w * 8192;  // 32 rows x 256 bytes per wave
+        OUT_BF16 ? static_cast<void*>(o.yh + (size_t)m0 * N)
+                 : static_cast<void*>((SPLIT && !second ? o.ws : o.y) + (size_t)m0 * N),
+        (short)0, EPI == EPI_QKV ? 0 : mrows * N * YE, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(SPLIT ? o.ws + (size_t)m0 * N : o.y, (short)0, SPLIT ? mrows * N * 4 : 0,
+                                          0x00020000);
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(SPLIT ? o.res + (size_t)m0 * N : nullptr), (short)0, SPLIT ? mrows * N * 4 : 0,
+        0x00020000);
+    // 32 rows x 256 bytes per wave (SPLIT: 16 KB per wave, the other half's sums and the residual)
+    char* stg = reinterpret_cast<char*>(&S[0][0][0]) + w * (SPLIT ? 16384 : 8192);
+    static_assert(!SPLIT || sizeof(S) >= 8 * 16384, "split staging");
     // read-back role of lane l: fp32 rows 4 k + l / 16 (k < 8), unit l % 16 (4 columns);
     // bf16 rows 8 k + l / 8 (k < 4), unit l % 8 (8 columns).  A buffer's range
     // check covers the vector offset only, so the whole offset goes there: the
@@ -405,17 +459,55 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
     };
 #pragma unroll
     for (int i = 0; i < MT; i++) {
-      // 1. this chunk into the wave's staging rows
+      // 1. this chunk into the wave's staging rows (SPLIT: the raw sums; the
+      // second half adds the other half's sums, the bias and the residual there)
+      if constexpr (SPLIT) {
+        if (second) {
+          // the other half's sums and the residual of the chunk by direct-to-LDS
+          // loads into the wave's 16 KB (sums, then residual), in the staging
+          // layout: load k, lane l fills row 4k + l / 16 at unit position l % 16
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the previous chunk's read-back is done
+#pragma unroll
+          for (int k = 0; k < 8; k++) {
+            const int cr = 4 * k + rrow0, uc = ru ^ (cr & 15);  // the piece's row and logical unit
+            const int lr = g * (BM / 2) + i * 32 + cr, c = n0 + q * 64 + 4 * uc;
+            const unsigned off = c < N ? (unsigned)((lr * N + c) * 4) : 0x80000000u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void*)(stg + 1024 * k), 16,
+                                                     off, 0, 0, 17);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rr, (__attribute__((address_space(3))) void*)(stg + 8192 + 1024 * k), 16, off, 0, 0, 0);
+          }
+          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int a = 0; a < 4; a++) {
+              const int u = (8 * j + 2 * a + efh) ^ (efr & 15);
+              float4* py = reinterpret_cast<float4*>(stg + efr * 256 + u * 16);
+              const float4 pv = *py, rv = *reinterpret_cast<const float4*>(stg + 8192 + efr * 256 + u * 16);
+              const float4 bc = *reinterpret_cast<const float4*>(&bias_s[q * 64 + j * 32 + 8 * a + 4 * efh]);
+              // ((own + other half) + bias) + residual: the same bits whichever half came first
+              float4 yv = make_float4(((acc[j][i][4 * a] + pv.x) + bc.x) + rv.x,
+                                      ((acc[j][i][4 * a + 1] + pv.y) + bc.y) + rv.y,
+                                      ((acc[j][i][4 * a + 2] + pv.z) + bc.z) + rv.z,
+                                      ((acc[j][i][4 * a + 3] + pv.w) + bc.w) + rv.w);
+              if (bad) yv = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+              *py = yv;
+            }
+        }
+      }
 #pragma unroll
       for (int j = 0; j < 2; j++)
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-          const float4 bc = *reinterpret_cast<const float4*>(&bias_s[q * 64 + j * 32 + 8 * a + 4 * efh]);
+          if (SPLIT && second) break;  // staged above
+          const float4 bc = SPLIT ? make_float4(0.f, 0.f, 0.f, 0.f)
+                                  : *reinterpret_cast<const float4*>(&bias_s[q * 64 + j * 32 + 8 * a + 4 * efh]);
           const float bcv[4] = {bc.x, bc.y, bc.z, bc.w};
           float v[4];
 #pragma unroll
           for (int b = 0; b < 4; b++) {
-            v[b] = acc[j][i][4 * a + b] + bcv[b];
+            v[b] = SPLIT ? acc[j][i][4 * a + b] : acc[j][i][4 * a + b] + bcv[b];
             if constexpr (EPI == EPI_GELU) v[b] = OUT_BF16 ? gelu_for_bf16(v[b]) : gelu_tanh(v[b]);
           }
           if constexpr (OUT_BF16) {
@@ -460,6 +552,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
         }
       }
     }
+    if constexpr (SPLIT) {
+      if (!second) {
+        // every wave's stores of the sums have completed; then the tile is marked ready
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) __hip_atomic_fetch_or(o.cnt + t, SPLIT_READY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
     // every wave is past its LDS reads and stores before the next tile's loads
     pp_sync<0>();
   }
@@ -487,11 +587,11 @@ static hipError_t launch_bm(hipStream_t st, int gm, int gn, const bf16_t* a, int
   return hipErrorInvalidValue;  // an epilogue combination no caller uses
 }
 
-template <int BM, int EPI, bool OUT_BF16>
+template <int BM, int EPI, bool OUT_BF16, bool SPLIT = false>
 static hipError_t launch_pp_tiles(hipStream_t st, int gm, int gn, int nb, const bf16_t* a, int M, int K,
                                   const bf16_t* Wt, int N, const float* bias, const GemmBf16Out& o) {
-  hipLaunchKernelGGL((k_gemm_bf16_pp<BM, EPI, OUT_BF16>), dim3(nb), dim3(512), 0, st, a, M, K, Wt, N, bias, o, gm,
-                     gn);
+  hipLaunchKernelGGL((k_gemm_bf16_pp<BM, EPI, OUT_BF16, SPLIT>), dim3(nb), dim3(512), 0, st, a, M, K, Wt, N, bias, o,
+                     gm, gn);
   return hipGetLastError();
 }
 
@@ -548,6 +648,30 @@ static hipError_t launch_any(hipStream_t st, const bf16_t* a, int M, int K, cons
   const int gm256 = (M + 255) / 256, gm128 = (M + 127) / 128;
   if (gm256 * gn >= 512) return launch_bm<256>(st, gm256, gn, a, M, K, Wt, N, bias, epi, o);
   return launch_bm<128>(st, gm128, gn, a, M, K, Wt, N, bias, epi, o);
+}
+
+hipError_t launch_gemm_bf16_split(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
+                                  const float* bias, const float* res, float* y, float* ws, size_t ws_floats,
+                                  int* cnt, int cnt_cap) {
+  if (!y || !res) return hipErrorInvalidValue;
+  // the split when 256 x 256 tiles leave CUs idle and two halves per tile fill them,
+  // each half a whole number of 64-deep K steps, the halves in XCD runs (8 divides
+  // the item count, so a tile's halves go to blocks b and b + 8); otherwise the
+  // unsplit kernels
+  const int gm = (M + 255) / 256, gn = (N + PBN - 1) / PBN, cus = pp_blocks(1 << 30);
+  auto al = [](const void* p, unsigned n) { return ((uintptr_t)p & (n - 1)) == 0; };
+  const bool split = a && Wt && M > 0 && K > 0 && K % (4 * TK) == 0 && N % 4 == 0 && ws && cnt &&
+                     (gm * gn) % 4 == 0 &&
+                     ws_floats >= (size_t)M * N && gm * gn <= cnt_cap && gm * gn < cus && 2 * gm * gn >= cus &&
+                     al(y, 16) && al(res, 16) && al(ws, 16) && (size_t)256 * K * 2 <= 0x7fffffffu &&
+                     (size_t)256 * N * 4 <= 0x7fffffffu;
+  if (!split) return launch_gemm_bf16(st, a, M, K, Wt, N, bias, EPI_NONE, res, y, nullptr);
+  GemmBf16Out o{};
+  o.res = res;
+  o.y = y;
+  o.ws = ws;
+  o.cnt = cnt;
+  return launch_pp_tiles<256, EPI_NONE, false, true>(st, gm, gn, pp_blocks(2 * gm * gn), a, M, K, Wt, N, bias, o);
 }
 
 hipError_t launch_gemm_bf16(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,

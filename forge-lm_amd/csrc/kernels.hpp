@@ -115,6 +115,18 @@ hipError_t launch_gemm_mfma(hipStream_t st, const float* a, int M, int K, const 
 hipError_t launch_gemm_bf16(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
                             const float* bias, int epi, const float* res, float* y, bf16_t* yh);
 
+// The residual form of launch_gemm_bf16 (y = a @ W + bias + res, fp32 y) with
+// the sum over K split in two halves on separate blocks when the product has too
+// few 256 x 256 tiles to fill the CUs (mlp.proj: N 1024, K 4096): the half that
+// finishes first leaves its partial sums in ws (M*N floats), the other adds them
+// (fp32 addition commutes, so the bits do not depend on which half is first).
+// cnt holds cnt_cap ints that are zero before the call and zero after it (one per
+// tile).  Calls sharing ws or cnt must not overlap.  Shapes the split does not
+// suit run as launch_gemm_bf16.
+hipError_t launch_gemm_bf16_split(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
+                                  const float* bias, const float* res, float* y, float* ws, size_t ws_floats,
+                                  int* cnt, int cnt_cap);
+
 // Outputs of the bf16 GEMM's epilogues (one set is used per launch).
 struct GemmBf16Out {
   const float* res;  // residual added to y, or null
@@ -125,6 +137,8 @@ struct GemmBf16Out {
   bf16_t* vc;
   RowSrc src;
   int T, H, ctx;
+  float* ws;  // K split in two: the first half's partial sums [M][N] (launch_gemm_bf16_split)
+  int* cnt;   // and one arrival counter per 256 x 256 tile, zero between launches
 };
 
 // The QKV projection of a window with the cache store fused (replaces the fp32

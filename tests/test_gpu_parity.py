@@ -494,6 +494,38 @@ def test_matmul_nn_bf16_pingpong_tiles(fhp, backend, M, K, N):
         buf.free()
 
 
+@pytest.mark.parametrize("M,K,N", [(8192, 4096, 1024), (8100, 2048, 1000), (4096, 4096, 2048)])
+def test_matmul_nn_bf16_split_k_accumulate(fhp, backend, M, K, N):
+    # accumulating bf16 products whose 256 x 256 tiles cover half the CUs or more
+    # but not all split K in two over separate blocks (C5's mlp.proj is the first
+    # case; the second is ragged in M and N; the third has 16 x 8 tiles): the
+    # second half to finish adds the first's sums, the bias and the old y.  Run
+    # twice: the tile counters must be left at zero for the next product.
+    r = np.random.default_rng(M + K + N + 2)
+    a = r.standard_normal((M, K)).astype(np.float32)
+    b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
+    y0 = r.standard_normal((M, N)).astype(np.float32)
+    a_used, _ = bf16_round(a)
+    b_used, b_bits = bf16_round(b)
+    prod = a_used.astype(np.float64) @ b_used.astype(np.float64)
+    scale = np.abs(a_used).astype(np.float64) @ np.abs(b_used).astype(np.float64)
+    bufa = fhp.DeviceBuffer.from_array(backend, a)
+    bufb = fhp.DeviceBuffer.from_array(backend, b_bits)
+    bufy = fhp.DeviceBuffer.from_array(backend, y0)
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=True, dtype="bf16")
+    got1 = bufy.read(np.float32, M * N).reshape(M, N)
+    ref1 = y0.astype(np.float64) + prod
+    tol1 = 1e-5 * (scale + np.abs(y0)) + 1e-6
+    assert np.all(np.abs(got1 - ref1) <= tol1), float(np.max(np.abs(got1 - ref1) / tol1))
+    backend.matmul_nn(bufa, bufb, bufy, M, K, N, accumulate=True, dtype="bf16")
+    got2 = bufy.read(np.float32, M * N).reshape(M, N)
+    ref2 = got1.astype(np.float64) + prod
+    tol2 = 1e-5 * (scale + np.abs(got1)) + 1e-6
+    assert np.all(np.abs(got2 - ref2) <= tol2), float(np.max(np.abs(got2 - ref2) / tol2))
+    for buf in (bufa, bufb, bufy):
+        buf.free()
+
+
 def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
     # Forge-220M shape with bf16 weights, reduced to a 64-token
     # prompt and 3 steps per sequence so the CPU oracle stays quick; the oracle runs
