@@ -188,7 +188,8 @@ def copy_calibration(mib: int, reps: int) -> dict:
 
 
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_step_c2_traffic.md")
-TRAFFIC_PROFILE_2 = os.path.join("profiles", "traffic_c3_c4_c5.md")
+TRAFFIC_PROFILE_2 = os.path.join("profiles", "traffic_c3_c4.md")
+TRAFFIC_PROFILE_C5 = os.path.join("profiles", "prefill_c5_traffic.md")
 
 
 def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
@@ -261,7 +262,7 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
         "config": {"workload": w["desc"], "batch": B, "prompt_len": P, "new_tokens": NEW},
     }
     if name == "c5":
-        c5_traffic, _, c5_build = profiled_traffic("prefill forward", TRAFFIC_PROFILE_2)
+        c5_traffic, _, c5_build = profiled_traffic("prefill forward", TRAFFIC_PROFILE_C5)
         flops = prefill_flops(c, min(P, ctx), B)
         tflops = flops / pre_s / 1e12
         pre_tok = B * min(P, ctx) / pre_s
@@ -278,7 +279,7 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
                          "flops_per_launch": flops, "launch_us": round(pre_s * 1e6, 1)},
         })
         if c5_traffic is not None:
-            out["roofline"]["traffic_source"] = f"{TRAFFIC_PROFILE_2} (counted on {c5_build})"
+            out["roofline"]["traffic_source"] = f"{TRAFFIC_PROFILE_C5} (counted on {c5_build})"
         # the timed unit is one prefill forward; value is its token rate
         out["steps"] = steps
     else:
