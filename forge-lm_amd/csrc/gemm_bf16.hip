@@ -270,6 +270,10 @@ __device__ __forceinline__ void pp_sync() {
 // counter, and a second half that finds the first on another XCD writes NaN
 // instead of sums it might not see.
 constexpr int SPLIT_READY = 0x10000;
+// The even item's share of K, in sixteenths: 7 / 16 lets most first halves store
+// their sums while the second halves still multiply (C5 4.68 against 4.71 ms per
+// window for 8 / 16 on one box; 6 / 16 4.76)
+constexpr int SPLIT_FIRST16 = 7;
 
 __device__ __forceinline__ int hw_xcc() {
   unsigned v;
@@ -297,12 +301,15 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
   const int g = w >> 2, q = w & 3;
   const int fr = lane & 31, fh = lane >> 5;
   const int lrow = lane >> 2, lpos = lane & 3;  // a load's lane i fills row i / 4, position i % 4
-  const int nk = SPLIT ? K / TK / 2 : K / TK;  // K steps per item
+  const int nkall = K / TK;
   for (int it = 0;; it++) {
     const int tt = runs ? bid / 8 + it * (nb / 8) : bid + it * nb;
     if (tt >= (runs ? ntiles / 8 : ntiles)) break;
     const int item = runs ? (bid % 8) * (ntiles / 8) + tt : tt;
-    const int t = SPLIT ? item >> 1 : item, ks0 = SPLIT ? (item & 1) * nk : 0;  // tile, first K step
+    // SPLIT: the first half (even item) takes SPLIT_FIRST16 / 16 of the K steps
+    const int kfirst = SPLIT ? nkall * SPLIT_FIRST16 / 16 : nkall;
+    const int t = SPLIT ? item >> 1 : item, ks0 = SPLIT ? (item & 1) * kfirst : 0;  // tile, first K step
+    const int nk = SPLIT ? ((item & 1) ? nkall - kfirst : kfirst) : nkall;  // K steps of this item
     const int m0 = (t / gn) * BM, n0 = (t % gn) * PBN;
     const int arows = min(BM, M - m0), brows = min(PBN, N - n0);
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
