@@ -113,7 +113,9 @@ __global__ __launch_bounds__(256) void k_layernorm(const float* __restrict__ in,
 
 // The same for d a multiple of 256, one wave per row, rounded to bf16: the row
 // stays in registers (VPL float4 per lane, coalesced 1 KB loads), mean and
-// variance are wave sums, the output goes out as 8-byte bf16 quads.
+// variance are wave sums, the output goes out as 8-byte bf16 quads.  w and b are
+// requested with the row (a load issued after the first output store would wait
+// for it: loads and stores share one completion counter).
 template <int VPL>
 __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __restrict__ in, int rows,
                                                              const float* __restrict__ w,
@@ -124,13 +126,18 @@ __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __rest
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const float4* xr = reinterpret_cast<const float4*>(in + (size_t)r * d);
-  float4 x[VPL];
-  float s = 0.f;
+  float4 x[VPL], wv[VPL], bv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; i++) x[i] = xr[i * 64 + lane];
 #pragma unroll
   for (int i = 0; i < VPL; i++) {
-    x[i] = xr[i * 64 + lane];
-    s += (x[i].x + x[i].y) + (x[i].z + x[i].w);
+    wv[i] = reinterpret_cast<const float4*>(w)[i * 64 + lane];
+    bv[i] = reinterpret_cast<const float4*>(b)[i * 64 + lane];
   }
+  __builtin_amdgcn_sched_barrier(0);  // the loads stay here, ahead of the reductions
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; i++) s += (x[i].x + x[i].y) + (x[i].z + x[i].w);
   const float mu = wave_sum_dpp(s) / (float)d;
   float v = 0.f;
 #pragma unroll
@@ -142,12 +149,10 @@ __global__ __launch_bounds__(256) void k_layernorm_rows_bf16(const float* __rest
   uint2* orow = reinterpret_cast<uint2*>(out + (size_t)r * d);
 #pragma unroll
   for (int i = 0; i < VPL; i++) {
-    const float4 wv = reinterpret_cast<const float4*>(w)[i * 64 + lane];
-    const float4 bv = reinterpret_cast<const float4*>(b)[i * 64 + lane];
-    const uint32_t lo = (uint32_t)bf16_rn(x[i].x * rs * wv.x + bv.x) |
-                        ((uint32_t)bf16_rn(x[i].y * rs * wv.y + bv.y) << 16);
-    const uint32_t hi = (uint32_t)bf16_rn(x[i].z * rs * wv.z + bv.z) |
-                        ((uint32_t)bf16_rn(x[i].w * rs * wv.w + bv.w) << 16);
+    const uint32_t lo = (uint32_t)bf16_rn(x[i].x * rs * wv[i].x + bv[i].x) |
+                        ((uint32_t)bf16_rn(x[i].y * rs * wv[i].y + bv[i].y) << 16);
+    const uint32_t hi = (uint32_t)bf16_rn(x[i].z * rs * wv[i].z + bv[i].z) |
+                        ((uint32_t)bf16_rn(x[i].w * rs * wv[i].w + bv[i].w) << 16);
     orow[i * 64 + lane] = make_uint2(lo, hi);
   }
 }
