@@ -175,6 +175,17 @@ __global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ 
   const int pbytes = (int)((size_t)S * M * N * 4);
   const __amdgpu_buffer_rsrc_t rp =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part), (short)0, pbytes, 0x00020000);
+  const size_t idx = (size_t)r * N + c;
+  // the column's bias, residual and LayerNorm weights are requested with the
+  // partials: issued later, each would cost a round trip of its own (the last ones
+  // behind the store of y: loads and stores share one completion counter)
+  float bc = 0.f, rc = 0.f, wc = 0.f, lbc = 0.f;
+  if (on) {
+    if (bias) bc = bias[c];
+    if (res) rc = res[idx];
+    wc = w[c];
+    lbc = b[c];
+  }
   float v = 0.f;
   for (int i0 = 0; i0 < S; i0 += 32) {
     float t[32];
@@ -186,10 +197,9 @@ __global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ 
 #pragma unroll
     for (int ii = 0; ii < 32; ii++) v += t[ii];
   }
-  const size_t idx = (size_t)r * N + c;
   if (on) {
-    if (bias) v += bias[c];
-    if (res) v += res[idx];
+    if (bias) v += bc;
+    if (res) v += rc;
     y[idx] = v;
   } else {
     v = 0.f;
@@ -197,7 +207,7 @@ __global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ 
   const float mu = block_sum<1024>(v, red) / (float)N;
   const float dd = on ? v - mu : 0.f;
   const float rs = 1.f / sqrtf(block_sum<1024>(dd * dd, red) / (float)N + eps);
-  if (on) out[idx] = dd * rs * w[c] + b[c];
+  if (on) out[idx] = dd * rs * wc + lbc;
 }
 
 // Split-K reduction of a qkv projection (sum + bias into qkv) fused with the KV
@@ -282,13 +292,15 @@ __global__ __launch_bounds__(256) void k_splitk_epilogue(const float* __restrict
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (size_t)M * N) return;
   const int n = (int)(idx % N);
+  // the bias and residual are requested with the partials (one round trip, not three)
+  const float bn = bias ? bias[n] : 0.f, rn = res ? res[idx] : 0.f;
   float s = 0.f;
   // partials summed in order; the unrolled loads of a batch are independent and go out together
 #pragma unroll 8
   for (int i = 0; i < S; i++) s += part[(size_t)i * M * N + idx];
-  if (bias) s += bias[n];
+  if (bias) s += bn;
   if (epi == EPI_GELU) s = gelu_tanh(s);
-  if (res) s += res[idx];
+  if (res) s += rn;
   y[idx] = s;
 }
 
