@@ -69,6 +69,9 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
     // writes the new K and V rows into the caches, which its loads below then read
     const size_t N3 = (size_t)3 * d, MN = (size_t)qp.M * N3;
     const float* p0 = qp.part + (size_t)b * N3;
+    // the bias is requested with the partials (one round trip, not two)
+    const float4 bb =
+        qp.bias ? *reinterpret_cast<const float4*>(qp.bias + h * 64 + d4) : make_float4(0.f, 0.f, 0.f, 0.f);
     float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll 8
     for (int i = 0; i < qp.S; i++) {
@@ -79,7 +82,6 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
       a.w += v.w;
     }
     if (qp.bias) {
-      const float4 bb = *reinterpret_cast<const float4*>(qp.bias + h * 64 + d4);
       a.x += bb.x;
       a.y += bb.y;
       a.z += bb.z;
@@ -90,10 +92,11 @@ __global__ __launch_bounds__(256) void k_attn_decode_wide(RowSrc src, const floa
     if ((unsigned)pos < (unsigned)ctx && c == pos / CHUNK) {
       if (tid < 128) {
         const int col = (tid < 64 ? d : 2 * d) + h * 64 + (tid & 63);
+        const float bcol = qp.bias ? qp.bias[col] : 0.f;  // requested with the partials
         float v = 0.f;
 #pragma unroll 8
         for (int i = 0; i < qp.S; i++) v += p0[i * MN + col];
-        if (qp.bias) v += qp.bias[col];
+        if (qp.bias) v += bcol;
         (tid < 64 ? kc : vc)[head + (size_t)pos * 64 + (tid & 63)] = from_f32<KT>(v);
       }
       __syncthreads();  // the new rows are stored before any wave reads them
