@@ -222,13 +222,17 @@ __global__ __launch_bounds__(256) void k_epilogue_qkv(const float* __restrict__ 
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (size_t)M * N) return;
   const int col = (int)(idx % N), r = (int)(idx / N);
+  // the bias and the step counter are requested with the partials (a load issued
+  // after the store of qkv would wait for it)
+  const float bc = bias ? bias[col] : 0.f;
+  const int step = *src.step;
   float a = 0.f;
 #pragma unroll 8
   for (int i = 0; i < S; i++) a += part[(size_t)i * M * N + idx];
-  if (bias) a += bias[col];
+  if (bias) a += bc;
   qkv[idx] = a;
   if (col < d) return;
-  const int pos = src.pos_off + src.pos_mul * *src.step + r % T;
+  const int pos = src.pos_off + src.pos_mul * step + r % T;
   if ((unsigned)pos >= (unsigned)ctx) return;
   const int hd = d / H, c = col < 2 * d ? col - d : col - 2 * d, h = c / hd, e = c % hd;
   const size_t dst = (((size_t)(r / T) * H + h) * ctx + pos) * hd + e;
