@@ -368,6 +368,16 @@ hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, 
   int S = 1;
   const int target = 2 * (cus > 0 ? cus : 256);
   while (gn * gm * S * 2 <= target && (K / BK) % (S * 2) == 0 && (size_t)S * 2 * M * N <= part_floats) S *= 2;
+  // attn.proj of batched decode (N = d: 6 column tiles at d 768) takes any divisor
+  // of its stage count up to 32 partials (the epilogue's loads in flight): 24 splits
+  // on 144 blocks instead of 8 on 48 (C4 495.7 -> 489.1 ms per generate on one box;
+  // the same rule for every split GEMM was slower)
+  if (kind == AOP_ATTN)
+    for (int s = std::min(32, K / BK); s > S; s--)
+      if ((K / BK) % s == 0 && gn * gm * s <= target && (size_t)s * M * N <= part_floats) {
+        S = s;
+        break;
+      }
   *splits = S;
   const int kchunk = K / S;
   dim3 grid(gn, gm, S);
