@@ -188,7 +188,8 @@ def copy_calibration(mib: int, reps: int) -> dict:
 
 
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_step_c2_traffic.md")
-TRAFFIC_PROFILE_2 = os.path.join("profiles", "traffic_c3_c4.md")
+TRAFFIC_PROFILE_2 = os.path.join("profiles", "decode_sampled_c3_traffic.md")
+TRAFFIC_PROFILE_C4 = os.path.join("profiles", "decode_batched_c4_traffic.md")
 TRAFFIC_PROFILE_C5 = os.path.join("profiles", "prefill_c5_traffic.md")
 
 
@@ -306,12 +307,12 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
             traffic, _, build = profiled_traffic(kernel, TRAFFIC_PROFILE_2)
             traffic_src = f"{TRAFFIC_PROFILE_2} (counted on {build})" if traffic is not None else None
         elif not persistent and name == "c4":
-            _, ratio, build = profiled_traffic(kernel, TRAFFIC_PROFILE_2)
+            _, ratio, build = profiled_traffic(kernel, TRAFFIC_PROFILE_C4)
             if ratio is not None:
                 # the counted HBM / algorithmic ratio applied to this run's windows
                 traffic = int(ratio * step_bytes * tokens_per_launch)
-                traffic_src = (f"{TRAFFIC_PROFILE_2}: HBM / algorithmic bytes {ratio:.4f} counted at windows "
-                               f"513..576 ({build}), times this run's algorithmic bytes")
+                traffic_src = (f"{TRAFFIC_PROFILE_C4}: HBM / algorithmic bytes {ratio:.4f} counted at windows "
+                               f"513..575 ({build}), times this run's algorithmic bytes")
         out.update({
             "decode_tok_s": round(B * n_dec / dec_s, 2),
             "decode_us_per_step": round(avg_step_s * 1e6, 2),
