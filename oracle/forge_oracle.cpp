@@ -19,9 +19,14 @@
 //                          weights and uniforms are generated once and fed to
 //                          both this oracle and the GPU, so GPU parity does
 //                          not depend on it.
-//   Pcg32 ................ pinned by the PCG32 reference formula (O'Neill 2014)
-//                          checked in Python against an independent big-int
-//                          restatement plus the unbiased-bound rejection rule.
+//   Pcg32 ................ pinned exactly by the published pcg-c demo output
+//                          (pcg32_srandom_r(42, 54): six raw outputs, 65 coin
+//                          flips with bound 2 and 33 dice rolls with bound 6),
+//                          whose seeding is TrainingRandom's procedure and whose
+//                          bounded draw is its rejection rule; also checked
+//                          against an independent big-int restatement.
+//   fill_normal .......... pinned exactly: the first Box-Muller pair of
+//                          new Random(1) from its published Next() values.
 //   gelu ................. pinned by CpuBackendTests.Gelu_KnownValues.
 //   layernorm ............ pinned by LayerNorm_NormalizesRows (closed forms).
 //   softmax .............. pinned by Softmax_RowsSumToOne incl. the 1000 case.
@@ -104,9 +109,11 @@ struct NetRandom {
 };
 
 // PCG32 as in src/LLM.Core/Training/TrainingRandom.cs:13-72 (prompt ids).
+// The increment is TrainingRandom's constant (:16); it is settable so the tests can
+// run the seeding procedure with the published pcg-c demo's stream (initseq 54).
 struct Pcg32 {
-    uint64_t state = 0, inc = 0xDA3E39CB94B95BDBull;
-    explicit Pcg32(int seed) {
+    uint64_t state = 0, inc;
+    explicit Pcg32(int seed, uint64_t increment = 0xDA3E39CB94B95BDBull) : inc(increment) {
         next_u32();
         state += (uint64_t)(uint32_t)seed;
         next_u32();
@@ -764,6 +771,13 @@ void or_net_random_doubles(int seed, int n, double* out) {
 void or_pcg32_ids(int seed, int max_excl, int n, int* out) {
     Pcg32 r(seed);
     for (int i = 0; i < n; i++) out[i] = r.next(max_excl);
+}
+
+// The same generator with a given increment: draw i is NextUInt32 when bounds[i] == 0,
+// else Next(bounds[i]) (TrainingRandom.cs:13-20, 33-46, 64-71).
+void or_pcg32_stream(int seed, uint64_t inc, int n, const int* bounds, uint32_t* out) {
+    Pcg32 r(seed, inc);
+    for (int i = 0; i < n; i++) out[i] = bounds[i] == 0 ? r.next_u32() : (uint32_t)r.next(bounds[i]);
 }
 
 int64_t or_param_count(int V, int ctx, int d, int L, int H) {

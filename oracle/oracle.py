@@ -41,6 +41,8 @@ def lib():
         L.or_set_threads.argtypes = [_c_int]
         L.or_net_random_doubles.argtypes = [_c_int, _c_int, _f64p]
         L.or_pcg32_ids.argtypes = [_c_int, _c_int, _c_int, _i32p]
+        L.or_pcg32_stream.argtypes = [_c_int, ctypes.c_uint64, _c_int, _i32p,
+                                      np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")]
         L.or_param_count.argtypes = [_c_int] * 5
         L.or_param_count.restype = ctypes.c_int64
         L.or_init_weights.argtypes = [_c_int] * 6 + [_f32p]
@@ -115,6 +117,15 @@ def net_random_doubles(seed: int, n: int) -> np.ndarray:
 def pcg32_ids(seed: int, max_excl: int, n: int) -> np.ndarray:
     out = np.empty(n, dtype=np.int32)
     lib().or_pcg32_ids(seed, max_excl, n, out)
+    return out
+
+
+def pcg32_stream(seed: int, increment: int, bounds) -> np.ndarray:
+    """TrainingRandom's seeding (TrainingRandom.cs:13-20) with a given odd increment;
+    draw i is NextUInt32 when bounds[i] == 0, else Next(bounds[i]) (:33-46)."""
+    b = np.ascontiguousarray(bounds, dtype=np.int32)
+    out = np.empty(b.size, dtype=np.uint32)
+    lib().or_pcg32_stream(seed, increment, b.size, b, out)
     return out
 
 

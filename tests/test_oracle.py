@@ -280,6 +280,77 @@ def test_net_random_published_values(oracle):
     assert abs(oracle.net_random_doubles(0, 1)[0] - 0.7262432699679598) < 1e-15
 
 
+# Published output of the pcg-c demo (pcg32-demo.c, M. O'Neill): pcg32_srandom_r(&rng, 42, 54)
+# is TrainingRandom's seeding procedure (state 0, one step, state += seed, one step;
+# TrainingRandom.cs:13-20) with the increment (54 << 1) | 1.  Its "Round 1" prints six raw
+# outputs, 65 coin flips (pcg32_boundedrand_r(&rng, 2) ? 'H' : 'T') and 33 dice rolls
+# (pcg32_boundedrand_r(&rng, 6) + 1); the bounded draw rejects values below -bound % bound,
+# the rule of TrainingRandom.Next (:33-46).
+PCG_DEMO_U32 = [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+PCG_DEMO_COINS = "HHTTTHTHHHTHTTTHHHHHTTTHHHTHTHTHTTHTTTHHHHHHTTTTHHTTTTTHTTTTTTTHT"
+PCG_DEMO_ROLLS = [3, 4, 1, 1, 2, 2, 3, 2, 4, 3, 2, 4, 3, 3, 5, 2, 3, 1, 3, 1, 5, 1, 4, 1, 5, 6, 4, 6, 6, 2, 6,
+                  3, 3]
+
+
+def _pcg_u32_variant(seed, inc, n, seed_first=False):
+    """A deliberately different seeding (the seed added before the first step), to show
+    the published vector tells it apart from TrainingRandom's."""
+    m = (1 << 64) - 1
+    st = [0]
+
+    def step():
+        old = st[0]
+        st[0] = (old * 6364136223846793005 + inc) & m
+        xs = (((old >> 18) ^ old) >> 27) & 0xFFFFFFFF
+        rot = old >> 59
+        return ((xs >> rot) | (xs << ((-rot) & 31))) & 0xFFFFFFFF
+
+    if seed_first:
+        st[0] = (st[0] + seed) & m
+        step()
+        step()
+    return [step() for _ in range(n)]
+
+
+def test_pcg32_published_demo_stream(oracle):
+    inc = (54 << 1) | 1
+    out = oracle.pcg32_stream(42, inc, [0] * 6 + [2] * 65 + [6] * 33)
+    assert [int(v) for v in out[:6]] == PCG_DEMO_U32
+    assert "".join("H" if v else "T" for v in out[6:71]) == PCG_DEMO_COINS
+    assert [int(v) + 1 for v in out[71:]] == PCG_DEMO_ROLLS
+    # the vector discriminates: adding the seed before the first step gives another stream
+    assert _pcg_u32_variant(42, inc, 6, seed_first=True) != PCG_DEMO_U32
+    # and the oracle's default increment is TrainingRandom's (:16)
+    np.testing.assert_array_equal(oracle.pcg32_stream(7, 0xDA3E39CB94B95BDB, [16384] * 32),
+                                  oracle.pcg32_ids(7, 16384, 32).astype(np.uint32))
+
+
+def test_fill_normal_first_pairs_exact(oracle):
+    # Tensor.FillNormal (Tensor.cs:79-91) from new Random(1), whose first three samples are
+    # published (534011718, 237820880, 1002897798; NextDouble = sample / int.MaxValue):
+    # tok_emb[0..1] are the first Box-Muller pair, computed in double, times the float std
+    # widened to double, then cast to float.
+    import math
+    c = oracle.Config(32, 8, 16, 1, 2)
+    w = oracle.init_weights(c, 1)
+    n1, n2, n3 = (v / 2147483647 for v in (534011718, 237820880, 1002897798))
+    std = float(np.float32(0.02))
+
+    def pair(u1, u2):
+        r = math.sqrt(-2.0 * math.log(u1))
+        return (np.float32(r * math.cos(2 * math.pi * u2) * std), np.float32(r * math.sin(2 * math.pi * u2) * std))
+
+    want = pair(1.0 - n1, n2)
+    assert (w[0], w[1]) == want  # bit for bit
+    # planted mistakes move these values: cos/sin swapped, u1 = NextDouble(), the draws taken
+    # in the other order, one member duplicated
+    assert (want[1], want[0]) != want
+    assert pair(n1, n2) != want and pair(1.0 - n2, n1) != want and want[0] != want[1]
+    # the second pair's radius is fixed by the third sample alone: u1 = 1 - NextDouble()
+    radius = math.hypot(float(w[2]), float(w[3])) / std
+    assert abs(radius - math.sqrt(-2.0 * math.log(1.0 - n3))) < 2e-6 * radius
+
+
 # ---- golden vectors --------------------------------------------------------------------------
 
 def test_golden_c1_greedy(oracle):
