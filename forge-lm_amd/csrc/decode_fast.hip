@@ -2008,7 +2008,12 @@ __global__ __launch_bounds__(NT, 1) void k_decode_step(KParams p) {
 hipError_t decode_sampled_occupancy(int* occ) {
   return hipOccupancyMaxActiveBlocksPerMultiprocessor(occ, k_decode_step<768, 12, true>, NT, 0);
 }
-hipError_t decode_sampled_launch(hipStream_t st, const void* kparams) {
+hipError_t decode_sampled_launch(hipStream_t st, const void* kparams, bool cooperative) {
+  if (cooperative) {
+    void* args[] = {const_cast<void*>(kparams)};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_decode_step<768, 12, true>), dim3(NB),
+                                      dim3(NT), args, 0, st);
+  }
   hipLaunchKernelGGL((k_decode_step<768, 12, true>), dim3(NB), dim3(NT), 0, st,
                      *static_cast<const KParams*>(kparams));
   return hipGetLastError();
@@ -2061,6 +2066,14 @@ __global__ void k_gather_bias(const float* __restrict__ src, const int* __restri
   if (i >= NB * ncol) return;
   const int b = i / ncol, j = i % ncol, col = map[i];
   out[b * bt + off + j] = col >= 0 ? src[col] : 0.f;
+}
+
+// Fault injection for the host's fallback (FORGE_HIP_INJECT_FUSED_FAILURE=1):
+// the launch's error word is set before it starts, as after a wait that exceeded
+// its spin limit, so every wait of the launch gives up at once and every block
+// runs to its end without waiting.
+__global__ void k_set_word(int* p, int v) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) *p = v;
 }
 
 __global__ void k_copy(const float* __restrict__ src, float* __restrict__ dst, int n) {
@@ -2175,6 +2188,14 @@ int FastDecode::init(const fh_model_desc& d, int compute_units) {
   sampled_ok = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_decode_step<kD, kH, true>, NT, 0) == hipSuccess &&
                occ >= 1 && decode_sampled_occupancy(&occ) == hipSuccess && occ >= 1;
   if (hipGetDevice(&device) != hipSuccess) return FH_ERR_HIP;
+  {
+    int co = 0;
+    cooperative = hipDeviceGetAttribute(&co, hipDeviceAttributeCooperativeLaunch, device) == hipSuccess && co != 0;
+    const char* ce = getenv("FORGE_HIP_COOPERATIVE");
+    if (ce && ce[0] == '0') cooperative = false;
+    const char* fe = getenv("FORGE_HIP_INJECT_FUSED_FAILURE");
+    inject_failure = fe && fe[0] == '1';
+  }
   {
     // the XCD-local hand-offs need 8 XCDs dealt blocks round-robin (blocks
     // 8k .. 8k+7 on distinct XCDs); keep the generic path otherwise
@@ -2334,7 +2355,27 @@ int FastDecode::enqueue(hipStream_t st, const Step& s) {
   k.top_k = s.top_k;
   k.ngram = s.ngram;
   static_assert(kD == 768 && kH == 12, "the sampled kernel's instantiation");
-  if (s.sampled) return decode_sampled_launch(st, &k) == hipSuccess ? FH_OK : FH_ERR_HIP;
+  if (inject_failure) {
+    // a spin-limit code of wait 1 (x), layer 0, block 0
+    hipLaunchKernelGGL(k_set_word, dim3(1), dim3(64), 0, st, k.err, (int)(0x80000000u | (1u << 24)));
+    if (hipGetLastError() != hipSuccess) return FH_ERR_HIP;
+  }
+  // The 256 blocks wait on each other, so they must all be resident at once: a
+  // cooperative launch guarantees it (or fails up front).  Stream capture records
+  // plain kernel nodes only; the captured per-step launches rely on the occupancy
+  // checked at init (one block per CU on >= 256 CUs) and on the session's stream
+  // being the only work on the device.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) return FH_ERR_HIP;
+  const bool co = cooperative && cap == hipStreamCaptureStatusNone;
+  if (s.sampled) return decode_sampled_launch(st, &k, co) == hipSuccess ? FH_OK : FH_ERR_HIP;
+  if (co) {
+    void* args[] = {&k};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_decode_step<kD, kH, false>), dim3(NB),
+                                      dim3(NT), args, 0, st) == hipSuccess
+               ? FH_OK
+               : FH_ERR_HIP;
+  }
   hipLaunchKernelGGL((k_decode_step<kD, kH, false>), dim3(NB), dim3(NT), 0, st, k);
   return hipGetLastError() == hipSuccess ? FH_OK : FH_ERR_HIP;
 }

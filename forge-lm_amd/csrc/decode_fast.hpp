@@ -10,7 +10,7 @@ namespace fh {
 // its own): its occupancy, and a launch of 256 blocks with the kernel's
 // parameter block (`kparams` points at it; it is copied at the launch).
 hipError_t decode_sampled_occupancy(int* occ);
-hipError_t decode_sampled_launch(hipStream_t st, const void* kparams);
+hipError_t decode_sampled_launch(hipStream_t st, const void* kparams, bool cooperative);
 
 // Device state of the persistent decode path for one session.  It runs one
 // batch-1 fp32 decode step per launch: all layers, the tied head and (in
@@ -74,6 +74,13 @@ struct FastDecode {
   // Whether a sampled launch can run these options with windows up to window_end ids.
   bool sampler_fits(int top_k, int window_end) const;
   bool sampled_ok = false;  // the sampled kernel fits on the device
+  // launches outside stream capture are cooperative (co-residency of the 256
+  // blocks guaranteed, or the launch fails) when the device supports it, unless
+  // FORGE_HIP_COOPERATIVE=0
+  bool cooperative = false;
+  // FORGE_HIP_INJECT_FUSED_FAILURE=1 (fault injection, for the fallback's test):
+  // every launch starts with its error word set, so its waits give up at once
+  bool inject_failure = false;
   void release();
 
  private:

@@ -58,6 +58,7 @@ static thread_local std::string g_err;
 // gen_collect's answer when a persistent sampled launch reported a case for the
 // per-step sampler (not returned across the C ABI: fh_generate repeats the generation)
 constexpr int kRetryPerStep = -100;
+constexpr int kRetryGeneric = -101;  // a fused launch failed: fh_generate re-runs on the generic kernels
 
 static int set_err(int code, const char* fmt, ...) {
   char buf[512];
@@ -182,10 +183,11 @@ struct GraphKey {
   const void* dump = nullptr;
   const void* uniforms = nullptr;
   uint64_t gen = 0;
+  bool fused = false;  // captured with the fused decode step
   bool operator==(const GraphKey& o) const {
     return kind == o.kind && B == o.B && P == o.P && max_new == o.max_new && top_k == o.top_k && ngram == o.ngram &&
            eos == o.eos && temperature == o.temperature && penalty == o.penalty && dump == o.dump &&
-           uniforms == o.uniforms && gen == o.gen;
+           uniforms == o.uniforms && gen == o.gen && fused == o.fused;
   }
 };
 
@@ -211,6 +213,7 @@ struct GenState {
   bool persistent = false, dump = false, sampled = false;
   bool persist_sampled = false;  // the persistent launches also draw (sampled kernel)
   bool deferred = false;  // sampled, uniforms supplied per fh_generate_next call
+  bool one_shot = false;  // inside fh_generate (not a stream of fh_generate_next calls)
   fh_sampling opts{};
   StepPlan plan;        // plan.opts points at opts
 };
@@ -858,6 +861,20 @@ int fh_context_info(fh_context* c, char* name, size_t name_len, uint64_t* total_
   return FH_OK;
 }
 
+int fh_context_memory(fh_context* c, uint64_t* free_bytes, uint64_t* sampler_scratch_bytes) {
+  if (!c) return set_err(FH_ERR_INVALID, "context is null");
+  if (free_bytes) {
+    HIP_TRY(hipSetDevice(c->device));
+    size_t fr = 0, tot = 0;
+    HIP_TRY(hipMemGetInfo(&fr, &tot));
+    *free_bytes = fr;
+  }
+  if (sampler_scratch_bytes)
+    *sampler_scratch_bytes = (uint64_t)(c->s_work ? (size_t)c->s_V * sizeof(float) : 0) +
+                             (c->s_ints ? (size_t)c->s_hist * sizeof(int) : 0) + (c->s_u ? sizeof(double) : 0);
+  return FH_OK;
+}
+
 int fh_buffer_alloc(fh_context* c, size_t bytes, void** out_dev) {
   if (!c || !out_dev) return set_err(FH_ERR_INVALID, "null argument");
   *out_dev = nullptr;
@@ -936,7 +953,8 @@ int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_de
     const int ncnt = big && res ? ((M + 255) / 256) * ((N + 255) / 256) : 0;
     char* tmp = nullptr;
     const size_t wbytes = (size_t)N * K * esz + (big ? (size_t)M * K * 2 : part_floats * 4);
-    HIP_TRY(hipMalloc(&tmp, (wbytes + 255) / 256 * 256 + ws_floats * 4 + (size_t)ncnt * 4));
+    // the tile counters are followed by the split's error word
+    HIP_TRY(hipMalloc(&tmp, (wbytes + 255) / 256 * 256 + ws_floats * 4 + (size_t)(ncnt + 1) * 4));
     float* part = reinterpret_cast<float*>(tmp + (size_t)N * K * esz);
     float* ws = reinterpret_cast<float*>(tmp + (wbytes + 255) / 256 * 256);
     int* cnt = reinterpret_cast<int*>(ws + ws_floats);
@@ -945,7 +963,7 @@ int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_de
       bf16_t* ah = wt + (size_t)N * K;
       e = launch_transpose<bf16_t>(st, static_cast<const bf16_t*>(b_dev), K, N, wt);
       if (e == hipSuccess) e = launch_round_bf16(st, a, (size_t)M * K, ah);
-      if (e == hipSuccess && res) e = hipMemsetAsync(cnt, 0, (size_t)ncnt * 4, st);
+      if (e == hipSuccess && res) e = hipMemsetAsync(cnt, 0, (size_t)(ncnt + 1) * 4, st);
       if (e == hipSuccess)
         e = res ? launch_gemm_bf16_split(st, ah, M, K, wt, N, nullptr, res, y, ws, ws_floats, cnt, ncnt)
                 : launch_gemm_bf16(st, ah, M, K, wt, N, nullptr, EPI_NONE, res, y, nullptr);
@@ -961,7 +979,13 @@ int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_de
                                     part, part_floats, c->props.multiProcessorCount);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    int split_err = 0;
+    if (e == hipSuccess && big && res) e = hipMemcpy(&split_err, cnt + ncnt, sizeof(int), hipMemcpyDeviceToHost);
     (void)hipFree(tmp);
+    if (e == hipSuccess && split_err)
+      return set_err(FH_ERR_HIP, "split-K GEMM: a tile's two K halves did not meet (%s; y is not valid)",
+                     (split_err & 1) ? "the wait for the first half exceeded its bound"
+                                     : "the halves ran on different XCDs");
   } else {
     e = bf ? launch_gemm<bf16_t>(st, a, M, K, static_cast<const bf16_t*>(b_dev), N, nullptr, EPI_NONE, res, y)
            : launch_gemm<float>(st, a, M, K, static_cast<const float*>(b_dev), N, nullptr, EPI_NONE, res, y);
@@ -1048,9 +1072,10 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
       (rc = dev_alloc(&sp->out_counts, B)))
     return fail(rc);
   if (sp->esize == 2) {
+    // one counter per tile, then the split's error word
     sp->gsplit_cap = (int)((rows + 255) / 256) * ((D + 255) / 256);
-    if ((rc = dev_alloc(&sp->gsplit, sp->gsplit_cap)) != FH_OK) return fail(rc);
-    const hipError_t he = hipMemset(sp->gsplit, 0, (size_t)sp->gsplit_cap * sizeof(int));
+    if ((rc = dev_alloc(&sp->gsplit, sp->gsplit_cap + 1)) != FH_OK) return fail(rc);
+    const hipError_t he = hipMemset(sp->gsplit, 0, (size_t)(sp->gsplit_cap + 1) * sizeof(int));
     if (he != hipSuccess) return fail(set_err(FH_ERR_HIP, "hipMemset: %s", hipGetErrorString(he)));
   }
   for (auto& e : sp->ev) {
@@ -1239,6 +1264,20 @@ static int validate_ids(const fh_session* s, const int32_t* ids, size_t n) {
   return FH_OK;
 }
 
+// After the stream has finished: the error word of the bf16 window path's split-K
+// GEMM (mlp.proj), cleared for the next call.  Non-zero means a tile's two halves
+// did not meet and its output is NaN.
+static int check_split_error(fh_session* s) {
+  if (!s->gsplit) return FH_OK;
+  int word = 0;
+  HIP_TRY(hipMemcpy(&word, s->gsplit + s->gsplit_cap, sizeof(int), hipMemcpyDeviceToHost));
+  if (word == 0) return FH_OK;
+  const int zero = 0;
+  HIP_TRY(hipMemcpy(s->gsplit + s->gsplit_cap, &zero, sizeof(int), hipMemcpyHostToDevice));
+  return set_err(FH_ERR_HIP, "split-K GEMM: a tile's two K halves did not meet (%s; results discarded)",
+                 (word & 1) ? "the wait for the first half exceeded its bound" : "the halves ran on different XCDs");
+}
+
 int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* logits_out) {
   if (!s || !ids || !logits_out) return set_err(FH_ERR_INVALID, "null argument");
   if (!s->loaded) return set_err(FH_ERR_STATE, "weights are not loaded");
@@ -1263,7 +1302,7 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
   FH_TRY(enqueue_window(s, T, p));
   HIP_TRY(hipMemcpyAsync(logits_out, s->logits, sizeof(float) * batch * s->d.vocab_size, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
-  return FH_OK;
+  return check_split_error(s);
 }
 
 // Validation (Sampler.cs:82-89, 169-175), buffers, prompt upload and the step
@@ -1290,6 +1329,7 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   g.P = P;
   g.max_new = max_new;
   g.opts = *opts;
+  g.one_shot = one_shot;
   if (max_new == 0) {
     g.active = true;
     return FH_OK;
@@ -1333,6 +1373,7 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   key.dump = s->dump;
   key.uniforms = s->uniforms;
   key.gen = s->buf_gen;
+  key.fused = s->use_fast();
   int rc = FH_OK;
   // which of steps 1..max_new-1 are cached decode steps (window fits) vs re-prefills
   for (int n = 1; n < max_new; n++) (P + n > C ? g.n_re : g.n_dec)++;
@@ -1412,6 +1453,10 @@ static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, flo
   if (logits_dump)
     HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * g.max_new * V, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
+  if (check_split_error(s) != FH_OK) {
+    g.active = false;
+    return FH_ERR_HIP;
+  }
   unsigned wait_code = 0;
   if (s->use_fast() && g.n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
     s->fast.reset();
@@ -1421,14 +1466,18 @@ static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, flo
     if (what == 11)
       return set_err(FH_ERR_HIP, "fused decode step: a token id outside [0, VocabSize) (results discarded)");
     if (what == 12)
-      return set_err(FH_ERR_HIP,
-                     "fused decode step: two blocks of one launch ran on the same XCD slot (block %u; the "
-                     "dispatcher no longer deals blocks round-robin over the XCDs; results discarded)",
-                     wait_code & 0xffff);
-    return set_err(FH_ERR_HIP,
-                   "fused decode step: a hand-off wait exceeded its spin limit (wait %u, layer %u, block %u; "
-                   "results discarded)",
-                   what, (wait_code >> 16) & 0xff, wait_code & 0xffff);
+      set_err(FH_ERR_HIP,
+              "fused decode step: two blocks of one launch ran on the same XCD slot (block %u; the "
+              "dispatcher no longer deals blocks round-robin over the XCDs; results discarded)",
+              wait_code & 0xffff);
+    else
+      set_err(FH_ERR_HIP,
+              "fused decode step: a hand-off wait exceeded its spin limit (wait %u, layer %u, block %u; "
+              "results discarded)",
+              what, (wait_code >> 16) & 0xff, wait_code & 0xffff);
+    // fh_generate repeats the generation on the generic kernels; a stream
+    // (fh_generate_next) has handed out earlier chunks and reports the error
+    return g.one_shot ? kRetryGeneric : FH_ERR_HIP;
   }
   // a sequence without EOS so far has produced every step enqueued
   for (int b = 0; b < B; b++)
@@ -1477,6 +1526,16 @@ int fh_generate(fh_session* s, const int32_t* prompts, int batch, int P, int max
     rc = generate_once(s, prompts, batch, P, max_new, opts, uniforms, out_ids, out_counts, logits_dump);
     s->no_sampled_fused = false;
     if (rc == FH_OK) s->route |= FH_ROUTE_RETRIED;
+  }
+  if (rc == kRetryGeneric) {
+    // a fused launch gave up (a hand-off wait past its spin limit, or its blocks
+    // not covering the XCD slots): the same generation again on the generic
+    // kernels, which need no co-resident blocks
+    const bool saved = s->fast_allowed;
+    s->fast_allowed = false;
+    rc = generate_once(s, prompts, batch, P, max_new, opts, uniforms, out_ids, out_counts, logits_dump);
+    s->fast_allowed = saved;
+    if (rc == FH_OK) s->route |= FH_ROUTE_FALLBACK;
   }
   return rc;
 }
@@ -1639,6 +1698,10 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 static std::mutex g_scratch_mu;
 static std::vector<unsigned char*> g_scratch_dev;  // per device id: the device address of `scratch`
+// one lock per device id, held for a whole fh_sample_logits_noalloc call: calls on
+// one device from several threads or contexts take turns on the shared array
+constexpr int kScratchLocks = 64;
+static std::mutex g_scratch_call_mu[kScratchLocks];
 
 // Resolves `scratch`'s address on the current device (once per device); called by
 // fh_context_create with the context's device current.
@@ -1668,7 +1731,10 @@ int fh_sample_logits_noalloc(fh_context* c, const float* logits_dev, int V, cons
     if ((size_t)c->device < g_scratch_dev.size()) base = g_scratch_dev[c->device];
   }
   if (!base) return set_err(FH_ERR_STATE, "no scratch address for device %d", c->device);
+  if (c->device >= kScratchLocks) return set_err(FH_ERR_RANGE, "device id %d >= %d", c->device, kScratchLocks);
   HIP_TRY(hipSetDevice(c->device));
+  // sample_row returns once the stream has finished, so the array is free again
+  std::lock_guard<std::mutex> g(g_scratch_call_mu[c->device]);
   return sample_row(c, logits_dev, V, history, n_hist, opts, u01, out_id, reinterpret_cast<float*>(base),
                     reinterpret_cast<int*>(base + kScratchInts), reinterpret_cast<double*>(base + kScratchU));
 }

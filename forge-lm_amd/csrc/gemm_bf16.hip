@@ -268,8 +268,13 @@ __device__ __forceinline__ void pp_sync() {
 // (continuing from the previous dispatch, so blocks b and b + 8 share one), the
 // two halves of a tile are such a pair, each adds its hardware XCD to the tile's
 // counter, and a second half that finds the first on another XCD writes NaN
-// instead of sums it might not see.
-constexpr int SPLIT_READY = 0x10000;
+// instead of sums it might not see.  Either failure (that, or a ready mark that
+// does not come within the wait's bound) also sets the error word o.err, which
+// the host reads after the stream has finished.  Whichever half touches a
+// tile's counter last returns it to zero: normally the second half once it has
+// seen the mark; after the second half gave up (SPLIT_GAVEUP), the first half
+// when it sets the mark, so no stale mark survives into the next launch.
+constexpr int SPLIT_READY = 0x10000, SPLIT_GAVEUP = 0x20000;
 // The even item's share of K, in sixteenths: 7 / 16 lets most first halves store
 // their sums while the second halves still multiply (C5 4.68 against 4.71 ms per
 // window for 8 / 16 on one box; 6 / 16 4.76)
@@ -422,8 +427,15 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
             ok = (__hip_atomic_load(o.cnt + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & SPLIT_READY) != 0;
             if (!ok) __builtin_amdgcn_s_sleep(2);
           }
+          // giving up: the mark may still have come in between (then the sums are
+          // there); otherwise the first half, setting it later, clears the counter
+          if (!ok)
+            ok = (__hip_atomic_fetch_or(o.cnt + t, SPLIT_GAVEUP, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                  SPLIT_READY) != 0;
+          if (ok) __hip_atomic_store(o.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
+          if ((!ok || !xok) && o.err)
+            __hip_atomic_fetch_or(o.err, ok ? 2 : 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           ready_s = ok;
-          __hip_atomic_store(o.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
         }
         __syncthreads();
       }
@@ -564,7 +576,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm_bf16_pp(const bf16_t* __restric
         // every wave's stores of the sums have completed; then the tile is marked ready
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (tid == 0) __hip_atomic_fetch_or(o.cnt + t, SPLIT_READY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0 &&
+            (__hip_atomic_fetch_or(o.cnt + t, SPLIT_READY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & SPLIT_GAVEUP))
+          __hip_atomic_store(o.cnt + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // the second half gave up
       }
     }
     // every wave is past its LDS reads and stores before the next tile's loads
@@ -662,13 +676,14 @@ hipError_t launch_gemm_bf16_split(hipStream_t st, const bf16_t* a, int M, int K,
                                   int* cnt, int cnt_cap) {
   if (!y || !res) return hipErrorInvalidValue;
   // the split when 256 x 256 tiles leave CUs idle and two halves per tile fill them,
-  // each half a whole number of 64-deep K steps, the halves in XCD runs (8 divides
-  // the item count, so a tile's halves go to blocks b and b + 8); otherwise the
-  // unsplit kernels
+  // each half a whole number of 64-deep K steps, both halves of a tile in one XCD's
+  // run of items: the 2 gm gn items are dealt to the 8 XCDs in runs of gm gn / 4,
+  // which must be even so that no run boundary falls between items 2t and 2t + 1
+  // (8 divides gm gn); otherwise the unsplit kernels
   const int gm = (M + 255) / 256, gn = (N + PBN - 1) / PBN, cus = pp_blocks(1 << 30);
   auto al = [](const void* p, unsigned n) { return ((uintptr_t)p & (n - 1)) == 0; };
   const bool split = a && Wt && M > 0 && K > 0 && K % (4 * TK) == 0 && N % 4 == 0 && ws && cnt &&
-                     (gm * gn) % 4 == 0 &&
+                     (gm * gn) % 8 == 0 &&
                      ws_floats >= (size_t)M * N && gm * gn <= cnt_cap && gm * gn < cus && 2 * gm * gn >= cus &&
                      al(y, 16) && al(res, 16) && al(ws, 16) && (size_t)256 * K * 2 <= 0x7fffffffu &&
                      (size_t)256 * N * 4 <= 0x7fffffffu;
@@ -678,6 +693,7 @@ hipError_t launch_gemm_bf16_split(hipStream_t st, const bf16_t* a, int M, int K,
   o.y = y;
   o.ws = ws;
   o.cnt = cnt;
+  o.err = cnt + cnt_cap;
   return launch_pp_tiles<256, EPI_NONE, false, true>(st, gm, gn, pp_blocks(2 * gm * gn), a, M, K, Wt, N, bias, o);
 }
 

@@ -120,9 +120,12 @@ hipError_t launch_gemm_bf16(hipStream_t st, const bf16_t* a, int M, int K, const
 // few 256 x 256 tiles to fill the CUs (mlp.proj: N 1024, K 4096): the half that
 // finishes first leaves its partial sums in ws (M*N floats), the other adds them
 // (fp32 addition commutes, so the bits do not depend on which half is first).
-// cnt holds cnt_cap ints that are zero before the call and zero after it (one per
-// tile).  Calls sharing ws or cnt must not overlap.  Shapes the split does not
-// suit run as launch_gemm_bf16.
+// cnt holds cnt_cap + 1 ints: one per tile, zero before the call and zero after
+// it, then an error word that stays zero unless a tile's halves failed to meet
+// (bit 0: the second half's bounded wait for the first gave up; bit 1: the halves
+// ran on different XCDs); such a tile's y is NaN, and the caller reads the word
+// once the stream has finished.  Calls sharing ws or cnt must not overlap.
+// Shapes the split does not suit run as launch_gemm_bf16.
 hipError_t launch_gemm_bf16_split(hipStream_t st, const bf16_t* a, int M, int K, const bf16_t* Wt, int N,
                                   const float* bias, const float* res, float* y, float* ws, size_t ws_floats,
                                   int* cnt, int cnt_cap);
@@ -139,6 +142,7 @@ struct GemmBf16Out {
   int T, H, ctx;
   float* ws;  // K split in two: the first half's partial sums [M][N] (launch_gemm_bf16_split)
   int* cnt;   // and one arrival counter per 256 x 256 tile, zero between launches
+  int* err;   // and the split's error word (see launch_gemm_bf16_split)
 };
 
 // The QKV projection of a window with the cache store fused (replaces the fp32

@@ -25,12 +25,12 @@ FH_DTYPE_F32 = 0
 FH_DTYPE_BF16 = 1
 # fh_last_route bits
 FH_ROUTE_FUSED_STEP, FH_ROUTE_FUSED_EPILOGUES, FH_ROUTE_ATTN_IN_PROJ, FH_ROUTE_UNFUSED = 1, 2, 4, 8
-FH_ROUTE_FUSED_SAMPLER, FH_ROUTE_RETRIED = 16, 32
+FH_ROUTE_FUSED_SAMPLER, FH_ROUTE_RETRIED, FH_ROUTE_FALLBACK = 16, 32, 64
 
 # Every symbol include/forge_hip.h declares (checked by the CPU tests).
 EXPORTS = (
     "fh_last_error", "fh_version", "fh_random_doubles", "fh_context_create", "fh_context_destroy",
-    "fh_context_info", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
+    "fh_context_info", "fh_context_memory", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
     "fh_buffer_copy", "fh_matmul_nn",
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_init_weights", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
@@ -100,6 +100,7 @@ def lib():
     L.fh_context_create.argtypes = [ctypes.c_int, P(vp)]
     L.fh_context_destroy.argtypes = [vp]
     L.fh_context_info.argtypes = [vp, ctypes.c_char_p, ctypes.c_size_t, P(ctypes.c_uint64), P(i32)]
+    L.fh_context_memory.argtypes = [vp, P(ctypes.c_uint64), P(ctypes.c_uint64)]
     L.fh_buffer_alloc.argtypes = [vp, ctypes.c_size_t, P(vp)]
     L.fh_buffer_free.argtypes = [vp, vp]
     L.fh_buffer_write.argtypes = [vp, vp, vp, ctypes.c_size_t]

@@ -94,6 +94,11 @@ int fh_context_create(int device, fh_context** out);
 int fh_context_destroy(fh_context* ctx);
 int fh_context_info(fh_context* ctx, char* name, size_t name_len, uint64_t* total_mem_bytes,
                     int32_t* compute_units);
+/* Memory figures for the banner and for callers that budget device memory: the
+ * device's free bytes (hipMemGetInfo) and the device bytes this context holds as
+ * fh_sample_logits' scratch (0 until its first call).  Either pointer may be NULL.
+ * (The CUDA backend's counterpart is its arena accounting, CudaBackend.cs:397-543.) */
+int fh_context_memory(fh_context* ctx, uint64_t* free_bytes, uint64_t* sampler_scratch_bytes);
 
 /* Device buffers for op-level callers: the residency half of the tensor contract
  * (CudaBackend's arena rent/return and Read/Write, CudaBackend.cs:397-543;
@@ -192,6 +197,9 @@ int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t
 #define FH_ROUTE_UNFUSED 8          /* one kernel per op */
 #define FH_ROUTE_FUSED_SAMPLER 16   /* the persistent kernel also drew the sampled ids (top-k sampling) */
 #define FH_ROUTE_RETRIED 32         /* ... and met an exact top-k tie, so the generation re-ran per step */
+#define FH_ROUTE_FALLBACK 64        /* a fused launch gave up (a hand-off wait past its spin limit, or its
+                                       blocks not covering the XCD slots): fh_generate re-ran the generation
+                                       on the generic kernels, whose ids it returned */
 int fh_last_route(fh_session* s, int32_t* route);
 
 /* Sampler.ApplyRepetitionControls + Sampler.Sample on one logit row already on
@@ -207,8 +215,9 @@ int fh_sample_logits(fh_context* ctx, const float* logits_dev, int V, const int3
  * one fixed array in device memory that each device holds until the process ends
  * (about 392 KB), so V may be at most FH_NOALLOC_MAX_VOCAB and n_hist at most
  * FH_NOALLOC_MAX_HISTORY (FH_ERR_RANGE otherwise).  Every call on one device shares
- * that array: calls that overlap on one device (from several threads or contexts)
- * race and must be serialised by the caller. */
+ * that array; the library serialises calls on one device (a per-device lock held for
+ * the whole call, which returns after the stream has finished), so overlapping calls
+ * from several threads or contexts take turns.  Device ids must be below 64. */
 #define FH_NOALLOC_MAX_VOCAB 65536
 #define FH_NOALLOC_MAX_HISTORY 32768
 int fh_sample_logits_noalloc(fh_context* ctx, const float* logits_dev, int V, const int32_t* history, int n_hist,

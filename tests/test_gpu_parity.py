@@ -494,13 +494,18 @@ def test_matmul_nn_bf16_pingpong_tiles(fhp, backend, M, K, N):
         buf.free()
 
 
-@pytest.mark.parametrize("M,K,N", [(8192, 4096, 1024), (8100, 2048, 1000), (4096, 4096, 2048)])
+@pytest.mark.parametrize("M,K,N", [(8192, 4096, 1024), (8100, 2048, 1000), (4096, 4096, 2048), (8704, 2048, 1024),
+                                   (8448, 4096, 1024), (11264, 1024, 768)])
 def test_matmul_nn_bf16_split_k_accumulate(fhp, backend, M, K, N):
     # accumulating bf16 products whose 256 x 256 tiles cover half the CUs or more
     # but not all split K in two over separate blocks (C5's mlp.proj is the first
-    # case; the second is ragged in M and N; the third has 16 x 8 tiles): the
-    # second half to finish adds the first's sums, the bias and the old y.  Run
-    # twice: the tile counters must be left at zero for the next product.
+    # case; the second is ragged in M and N; the third has 16 x 8 tiles; the fourth
+    # 34 x 4 tiles, XCD runs of 34 items): the second half to finish adds the first's
+    # sums, the bias and the old y.  The last two have 33 x 4 and 44 x 3 tiles,
+    # whose XCD runs of 33 items would put a tile's two halves on different XCDs,
+    # so they must run unsplit.  Run twice: the tile counters must be left at zero
+    # for the next product (and the split's error word at zero: matmul_nn raises
+    # otherwise).
     r = np.random.default_rng(M + K + N + 2)
     a = r.standard_normal((M, K)).astype(np.float32)
     b = (r.standard_normal((K, N)) * 0.05).astype(np.float32)
@@ -907,6 +912,48 @@ def test_in_kernel_sampler_matches_per_step_sampler(fhp, oracle, backend, T, k, 
         assert oracle.sample(adj, T, k, float(u[i])) == ids[i], i
         seq.append(int(ids[i]))
     m.dispose()
+
+
+@pytest.mark.parametrize("mode", ["greedy", "sampled"])
+def test_fused_launch_failure_falls_back_to_generic_kernels(fhp, oracle, backend, monkeypatch, mode):
+    """FORGE_HIP_INJECT_FUSED_FAILURE=1 (read at session creation) starts every fused
+    launch with its error word set, as after a hand-off wait past its spin limit: every
+    wait of the launch gives up at once and every block runs to its end.  fh_generate
+    then repeats the whole generation on the generic kernels (FH_ROUTE_FALLBACK), whose
+    ids equal a session built for the generic kernels and, greedy, the oracle's.  A
+    stream (fh_generate_next) has handed out earlier chunks, so it reports the error."""
+    N = fhp._native
+    shape = (16384, 1024, 768, 2, 12)
+    monkeypatch.setenv("FORGE_HIP_INJECT_FUSED_FAILURE", "1")
+    m, oc, w = make_model(fhp, oracle, backend, shape, 71)
+    monkeypatch.delenv("FORGE_HIP_INJECT_FUSED_FAILURE")
+    monkeypatch.setenv("FORGE_HIP_FUSED_DECODE", "0")
+    g, _, _ = make_model(fhp, oracle, backend, shape, 71)
+    monkeypatch.delenv("FORGE_HIP_FUSED_DECODE")
+    prompt = fhp.TrainingRandom(17).ids(shape[0], 40)
+    n = 60
+    if mode == "greedy":
+        args = (0.0, 0, None)
+        kw = {}
+    else:
+        kw = dict(repetition_penalty=1.1, no_repeat_ngram_size=4)
+    def run(model):
+        a = args if mode == "greedy" else (0.7, 30, fhp.Random(3))
+        return fhp.Sampler.generate(model, prompt, n, *a, **kw)
+    ids = run(m)
+    rt = route(fhp)
+    assert rt & N.FH_ROUTE_FALLBACK and not rt & (N.FH_ROUTE_FUSED_STEP | N.FH_ROUTE_FUSED_SAMPLER), rt
+    want = run(g)
+    assert not route(fhp) & N.FH_ROUTE_FALLBACK
+    np.testing.assert_array_equal(ids, want)
+    if mode == "greedy":
+        np.testing.assert_array_equal(ids, oracle.generate(oc, w, prompt, n))
+        with pytest.raises(fhp.HipError, match="spin limit"):
+            list(fhp.Sampler.generate_stream(m, prompt, n, 0.0, 0, None, chunk=16))
+    # a later generation on the same session fails over again, from a clean state
+    np.testing.assert_array_equal(run(m), want)
+    m.dispose()
+    g.dispose()
 
 
 def test_in_kernel_sampler_ties_repeat_the_generation_per_step(fhp, oracle, backend):

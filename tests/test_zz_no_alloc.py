@@ -30,7 +30,8 @@ def _draw(fhp, fn, be, dev, V, hist, T, k, u, pen, ng):
 def test_noalloc_sampler_matches_allocating_sampler(fhp, first_V, second_V):
     N = fhp._native
     lib = N.lib()
-    be = fhp.HipBackend(0)
+    be = fhp.HipBackend(0)  # calls only the no-allocation entry point
+    ref = fhp.HipBackend(0)  # the allocating sampler, on a context of its own
     rng = np.random.default_rng(first_V + second_V)
     opts = [(0.0, 0, 1.0, 0), (0.7, 30, 1.1, 4), (1.0, 0, 2.0, 1), (0.9, 1, 1.0, 2), (0.8, 5000, 1.3, 3)]
     for T, k, pen, ng in opts:
@@ -40,11 +41,38 @@ def test_noalloc_sampler_matches_allocating_sampler(fhp, first_V, second_V):
             hist = rng.integers(0, min(V, 60), size=n_hist).astype(np.int32)
             u = float(rng.random())
             dev = fhp.DeviceBuffer.from_array(be, lg)
-            want = _draw(fhp, lib.fh_sample_logits, be, dev, V, hist, T, k, u, pen, ng)
+            want = _draw(fhp, lib.fh_sample_logits, ref, dev, V, hist, T, k, u, pen, ng)
             got = _draw(fhp, lib.fh_sample_logits_noalloc, be, dev, V, hist, T, k, u, pen, ng)
             dev.free()
             assert got == want, (V, n_hist, T, k, pen, ng, got, want)
             assert 0 <= got < V
+    # the no-allocation calls never used the context's own (allocated) scratch
+    assert be.memory()[1] == 0 and ref.memory()[1] > 0
+    be.dispose()
+    ref.dispose()
+
+
+def test_noalloc_sampler_allocates_nothing(fhp):
+    # a fresh context that only ever calls the no-allocation entry point: after one
+    # warm-up call (which loads the library's kernels), calls at the largest sizes and
+    # smaller ones leave the device's free memory and the context's scratch unchanged
+    lib = fhp._native.lib()
+    be = fhp.HipBackend(0)
+    rng = np.random.default_rng(5)
+    rows = {V: fhp.DeviceBuffer.from_array(be, (rng.standard_normal(V) * 2).astype(np.float32))
+            for V in (65536, 16384, 100)}
+    _draw(fhp, lib.fh_sample_logits_noalloc, be, rows[100], 100, [1, 2], 0.7, 5, 0.3, 1.1, 2)
+    free0, scr0 = be.memory()
+    for V, n_hist in ((65536, 32768), (100, 10), (16384, 5000), (65536, 32768), (16384, 0)):
+        hist = rng.integers(0, V, size=n_hist).astype(np.int32)
+        for T, k, pen, ng in ((0.0, 0, 1.0, 0), (0.8, 40, 1.2, 3)):
+            got = _draw(fhp, lib.fh_sample_logits_noalloc, be, rows[V], V, hist, T, k, float(rng.random()), pen, ng)
+            assert 0 <= got < V
+    free1, scr1 = be.memory()
+    assert scr0 == 0 and scr1 == 0
+    assert free1 == free0, (free0, free1)
+    for b in rows.values():
+        b.free()
     be.dispose()
 
 
