@@ -14,14 +14,18 @@ fused launch runs all 255 cached greedy steps) over its duration, timed with
 HIP events on the session stream inside the library.
 cpu_baseline: the oracle's restatement of the reference CPU algorithm
 (full-window recompute per token, Sampler.Generate semantics) on this host's
-cores (up to the 16 CPUs a GPU job is given on this pool), timed on the first
-tokens of the same workload and extrapolated to the whole run by the FLOPs of
-each step's window.
+cores (up to the 16 CPUs a GPU job is given on this pool): the whole C2
+workload; for the other configurations the first tokens of the same workload,
+extrapolated to the whole run by the FLOPs of each step's window.
 
 The default line also carries the rest of BASELINE's metric, measured in the
-same run: "bs32_decode" (config 4, batch 32) and "prefill" (config 5, bf16
-prefill), each with its own roofline (--no-extra leaves them out).  Each
-configuration also runs alone:
+same run: "sampled_decode" (config 3), "bs32_decode" (config 4, batch 32) and
+"prefill" (config 5, bf16 prefill), each with its own roofline and CPU baseline
+(a capped sample, extrapolated), and "stream": the drop-in seam as the CLI drives
+it (Sampler.generate_stream at the generate command's sampling defaults) against
+one fh_generate call (--no-extra leaves these out).  roofline.achievable is this
+box's copy and read bandwidth measured in the same run.  Each configuration also
+runs alone:
   --workload c3  sampling path (T 0.7, top-k 30, penalty 1.1, no-repeat 4-gram),
                  prompt 32 + 512 tokens; roofline over one decode step
   --workload c4  batch 32, prompts 512 (PCG32 seeds 42 + b) + 512 greedy;
@@ -32,6 +36,7 @@ configuration also runs alone:
                  = prefill FLOPs / prefill time against the bf16 MFMA peak
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--workload c2|c3|c4|c5]
+                       [--new N] [--prompt P] [--copy-calibration MIB]
 """
 from __future__ import annotations
 
@@ -151,15 +156,19 @@ def cpu_baseline(name: str, w: dict, prompts, gpu_ids, budget_tokens: int):
     ctx = w["shape"]["context_length"]
     cost = [window_flops(w["shape"], min(w["prompt"] + j, ctx)) for j in range(w["new"])]
     full_s = dt * sum(cost) / sum(cost[:n]) * w["batch"]
+    whole = n == w["new"] and w["batch"] == 1
     what = "sequence 0 of %d, " % w["batch"] if w["batch"] > 1 else ""
     out = {
         "value": w["batch"] * w["new"] / full_s, "unit": "tok/s", "cores": threads, "kind": "port",
         "host_cpus": nproc, "cpu_model": model_name,
         "sample": (f"reference CPU algorithm (C++ restatement, full-window recompute per token as "
+                   f"Sampler.Generate does) on the {name.upper()} weights and prompt: the whole workload "
+                   f"({w['new']} tokens) ran in {dt:.1f} s on {threads} threads" if whole else
+                   f"reference CPU algorithm (C++ restatement, full-window recompute per token as "
                    f"Sampler.Generate does) on the {name.upper()} weights and prompt: {what}steps 0..{n - 1} "
                    f"of {w['new']} ran in {dt:.1f} s on {threads} threads ({n / dt:.3g} tok/s); value = the "
                    f"whole workload ({w['batch']} x {w['new']} tokens) extrapolated by the FLOPs of each "
-                   f"step's window: {full_s:.0f} s"),
+                   f"step's window: {full_s:.0f} s (cap: {n} steps of sequence 0)"),
         "sample_tok_s": n / dt,
         "ids_match_gpu": bool((np.asarray(ids) == np.asarray(gpu0)[:n]).all()),
     }
@@ -170,21 +179,34 @@ def cpu_baseline(name: str, w: dict, prompts, gpu_ids, budget_tokens: int):
 
 
 def copy_calibration(mib: int, reps: int) -> dict:
-    """Times the library's plain copy kernel (fh_buffer_copy) on `mib` MiB: the
+    """Times the library's plain copy kernel (fh_buffer_copy) on `mib` MiB -- the
     known-size kernel whose FETCH_SIZE / WRITE_SIZE counters scale the decode
-    kernel's counters to bytes."""
+    kernel's counters to bytes -- and its read-only pass (fh_buffer_checksum, one
+    read of every byte): what this box's HBM sustains for a plain copy and a plain
+    read, next to the vendor peak."""
     import forge_hip as fhp
     nbytes = mib << 20
     be = fhp.HipBackend(0)
     src, dst = fhp.DeviceBuffer(be, nbytes), fhp.DeviceBuffer(be, nbytes)
     dst.copy_from(src)  # warm-up
     ms = [dst.copy_from(src) for _ in range(reps)]
+    src.checksum()
+    rms = [src.checksum()[1] for _ in range(reps)]
     src.free()
     dst.free()
     be.dispose()
-    best = min(ms)
+    best, rbest = min(ms), min(rms)
     return {"copy_bytes": nbytes, "reps": reps, "ms_min": round(best, 4), "ms_mean": round(sum(ms) / len(ms), 4),
-            "read_plus_write_GBs": round(2 * nbytes / best / 1e6, 1)}
+            "read_plus_write_GBs": round(2 * nbytes / best / 1e6, 1),
+            "read_ms_min": round(rbest, 4), "read_GBs": round(nbytes / rbest / 1e6, 1)}
+
+
+def achievable(reps: int = 5) -> dict:
+    """The box's sustained HBM rates measured in this run (1 GiB, best of `reps`)."""
+    c = copy_calibration(1024, reps)
+    return {"copy_read_plus_write_GBs": c["read_plus_write_GBs"], "read_GBs": c["read_GBs"],
+            "how": "fh_buffer_copy (grid-stride 16-byte copy) and fh_buffer_checksum (4 loads in flight per "
+                   "thread) on 1 GiB, best of %d; frac_of_achievable = achieved / read_GBs" % reps}
 
 
 TRAFFIC_PROFILE = os.path.join("profiles", "decode_step_c2_traffic.md")
@@ -212,7 +234,8 @@ def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
     return value, ratio, build
 
 
-def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: int = 0) -> dict:
+def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: int = 0, prompt: int = 0,
+                 cpu_budget: int = 0) -> dict:
     import numpy as np
     import forge_hip as fhp
 
@@ -220,6 +243,9 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
     if new:
         w["new"] = new
         w["desc"] += f" (shortened to {new} new tokens)"
+    if prompt:
+        w["prompt"] = prompt
+        w["desc"] += f" (prompt length {prompt}, a profiling run)"
     c = w["shape"]
     cfg = fhp.ModelConfig(**c)
     be = fhp.HipBackend(0)
@@ -335,11 +361,66 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
             out["metric"] = "decode tok/s, Forge-98M shape fp32 bs32 (prompt 512 + 512 greedy)"
     out["device"] = be.device_name
     if with_cpu:
-        budget = args.cpu_tokens if args.cpu_tokens else {"c2": 96, "c3": 96, "c4": 12, "c5": 2}[name]
+        # C2 runs the whole workload (BASELINE's CPU plan); the others a capped sample
+        budget = cpu_budget or args.cpu_tokens or {"c2": 256, "c3": 96, "c4": 12, "c5": 2}[name]
         out["cpu_baseline"] = cpu_baseline(name, w, prompts, ids, budget)
     model.dispose()
     be.dispose()
     return out
+
+
+def run_stream(steps: int, warmup: int) -> dict:
+    """The drop-in seam as the CLI drives it: Sampler.generate_stream (fh_generate_begin /
+    fh_generate_next, 16 steps per call) at the `generate` command's defaults -- temperature
+    0.8, top-k 40, no repetition controls, the tokenizer's EOS id set (Program.cs:642-644,
+    671-673) -- on the C2 shape and prompt, against one fh_generate call with the same
+    options.  The EOS id is one the run never draws, so every one of the 256 steps runs
+    (a model that emits no EOS within --tokens)."""
+    import ctypes
+    import numpy as np
+    import forge_hip as fhp
+    N = fhp._native
+    w = WORKLOADS["c2"]
+    cfg = fhp.ModelConfig(**w["shape"])
+    be = fhp.HipBackend(0)
+    model = fhp.GptModel(cfg, be, seed=1234)
+    prompt = prompts_for("c2", w, cfg.vocab_size)
+    NEW, T, K, CHUNK = w["new"], 0.8, 40, 16
+    drawn = set(int(i) for i in fhp.Sampler.generate(model, prompt, NEW, T, K, fhp.Random(1)))
+    eos = min(set(range(cfg.vocab_size)) - drawn)
+
+    def one():
+        return list(fhp.Sampler.generate(model, prompt, NEW, T, K, fhp.Random(1), eos))
+
+    def stream():
+        return list(fhp.Sampler.generate_stream(model, prompt, NEW, T, K, fhp.Random(1), eos, chunk=CHUNK))
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            ids = fn()
+        return ids, (time.perf_counter() - t0) / steps
+
+    ids_one, s_one = timed(one)
+    ids_stream, s_stream = timed(stream)
+    route = ctypes.c_int32()
+    N.check(N.lib().fh_last_route(model.handle, ctypes.byref(route)))
+    model.dispose()
+    be.dispose()
+    return {
+        "metric": "decode tok/s through Sampler.generate_stream, Forge-98M shape fp32 bs1, CLI sampling defaults",
+        "value": round(NEW / s_stream, 2), "unit": "tok/s", "steps": steps, "warmup": warmup,
+        "config": {"workload": f"C2 shape and prompt (64 ids), 256 tokens, temperature {T}, top-k {K}, penalty 1, "
+                               f"no n-gram ban, EOS id {eos} (never drawn), {CHUNK} steps per fh_generate_next, "
+                               f"Random(1) uniforms"},
+        "stream_us_per_token": round(s_stream / NEW * 1e6, 2),
+        "one_shot_us_per_token": round(s_one / NEW * 1e6, 2),
+        "stream_over_one_shot": round(s_stream / s_one, 4),
+        "ids_equal_one_shot": ids_stream == ids_one and len(ids_one) == NEW,
+        "in_kernel_sampler": bool(route.value & N.FH_ROUTE_FUSED_SAMPLER),
+    }
 
 
 def main():
@@ -356,7 +437,9 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=0,
                     help="tokens of the workload the CPU baseline runs (default: about 10-25 s on 16 cores)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only time the plain copy kernel on MIB MiB and print its line")
+                    help="only time the plain copy kernel (and the read-only pass) on MIB MiB and print its line")
+    ap.add_argument("--prompt", type=int, default=0,
+                    help="prompt length instead of the workload's (profiling runs, e.g. C4 near window 1023)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs one GPU only: the token loop of one batch-1 sequence is a single-GPU "
@@ -366,15 +449,23 @@ def main():
     if args.copy_calibration:
         print(json.dumps(copy_calibration(args.copy_calibration, max(1, args.steps))), flush=True)
         return
-    line = run_workload(args.workload, args, args.steps, args.warmup, not args.no_cpu, args.new)
-    if args.workload == "c2" and not args.no_extra and not args.new:
-        # the rest of the metric ("bs1/bs32 ... prefill tok/s"), two timed passes each
+    line = run_workload(args.workload, args, args.steps, args.warmup, not args.no_cpu, args.new, args.prompt)
+    ach = achievable()
+    if "roofline" in line and line["roofline"]["unit"] == "GB/s":
+        line["roofline"]["achievable"] = ach
+        line["roofline"]["frac_of_achievable_read"] = round(line["roofline"]["achieved"] / ach["read_GBs"], 4)
+    if args.workload == "c2" and not args.no_extra and not args.new and not args.prompt:
+        # the rest of the metric ("bs1/bs32 ... prefill tok/s"), two timed passes each, each
+        # with its CPU baseline (a capped sample, extrapolated; the cap is in its text)
         keep = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline",
                 "decode_tok_s", "decode_us_per_step", "prefill_tok_s", "decode_tok_s_reprefill",
-                "reprefill_ms_per_step", "whole_job_tok_s", "metric")
-        for key, wl in (("bs32_decode", "c4"), ("prefill", "c5")):
-            sub = run_workload(wl, args, 2, 1, False)
+                "reprefill_ms_per_step", "whole_job_tok_s", "metric", "cpu_baseline")
+        for key, wl in (("sampled_decode", "c3"), ("bs32_decode", "c4"), ("prefill", "c5")):
+            sub = run_workload(wl, args, 2, 1, not args.no_cpu)
+            if "roofline" in sub and sub["roofline"]["unit"] == "GB/s":
+                sub["roofline"]["frac_of_achievable_read"] = round(sub["roofline"]["achieved"] / ach["read_GBs"], 4)
             line[key] = {k: sub[k] for k in keep if k in sub}
+        line["stream"] = run_stream(2, 1)
     print(json.dumps(line), flush=True)
 
 

@@ -70,6 +70,8 @@ struct FastDecode {
   // FH_ERR_HIP when a wait of the last launches gave up; *code (optional)
   // says which: 1 << 31 | wait << 24 | layer << 16 | block.
   int check_error(unsigned* code = nullptr);
+  // The device word check_error reads (for an asynchronous copy on the stream).
+  const int* error_word() const { return reinterpret_cast<const int*>(ctl) + 16; }
   int reset();  // fresh launch counter, cleared hand-off area and error word
   // Whether a sampled launch can run these options with windows up to window_end ids.
   bool sampler_fits(int top_k, int window_end) const;

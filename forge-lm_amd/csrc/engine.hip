@@ -59,6 +59,7 @@ static thread_local std::string g_err;
 // per-step sampler (not returned across the C ABI: fh_generate repeats the generation)
 constexpr int kRetryPerStep = -100;
 constexpr int kRetryGeneric = -101;  // a fused launch failed: fh_generate re-runs on the generic kernels
+constexpr int kResumePerStep = -102;  // a stream's in-kernel sampler met a tie: resume on the per-step sampler
 
 static int set_err(int code, const char* fmt, ...) {
   char buf[512];
@@ -253,6 +254,10 @@ struct fh_session {
   size_t out_cap = 0;
   double* uniforms = nullptr;
   size_t uni_cap = 0;
+  // pinned host staging of a generation's results: ids [B * max_new], counts [B],
+  // then the fused kernel's and the split-K GEMM's error words (one stream sync)
+  int32_t* hstage = nullptr;
+  size_t hstage_cap = 0;
   float* dump = nullptr;
   size_t dump_cap = 0;
   uint64_t buf_gen = 1;
@@ -931,6 +936,37 @@ int fh_buffer_copy(fh_context* c, void* dst_dev, const void* src_dev, size_t byt
   return FH_OK;
 }
 
+int fh_buffer_checksum(fh_context* c, const void* src_dev, size_t bytes, uint64_t* sum_out, float* ms_out) {
+  if (!c || !src_dev || !sum_out) return set_err(FH_ERR_INVALID, "null argument");
+  if ((uintptr_t)src_dev % 16) return set_err(FH_ERR_INVALID, "the device buffer must be 16-byte aligned");
+  if (bytes % 4) return set_err(FH_ERR_INVALID, "bytes (%zu) must be a multiple of 4", bytes);
+  HIP_TRY(hipSetDevice(c->device));
+  // eight blocks per CU (a whole number of passes over most buffers), at most one per 4 KB
+  const int nparts = (int)std::max<size_t>(1, std::min<size_t>({(size_t)kChecksumParts,
+                                                                 (size_t)c->props.multiProcessorCount * 8,
+                                                                 (bytes + 4095) / 4096}));
+  unsigned long long* dbuf = nullptr;
+  FH_TRY(dev_alloc(&dbuf, (size_t)nparts + 1));
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = hipSuccess;
+  if (ms_out) {
+    e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipEventRecord(e0, c->stream);
+  }
+  if (e == hipSuccess) e = launch_checksum(c->stream, src_dev, bytes, dbuf + 1, nparts, dbuf, e1);
+  unsigned long long h = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(&h, dbuf, sizeof h, hipMemcpyDeviceToHost, c->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+  if (e == hipSuccess && ms_out) e = hipEventElapsedTime(ms_out, e0, e1);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  dev_free(dbuf);
+  HIP_TRY(e);
+  *sum_out = h;
+  return FH_OK;
+}
+
 int fh_matmul_nn(fh_context* c, const void* a_dev, const void* b_dev, void* y_dev, int M, int K, int N, int dtype,
                  int accumulate) {
   if (!c || !a_dev || !b_dev || !y_dev) return set_err(FH_ERR_INVALID, "null argument");
@@ -1112,6 +1148,8 @@ int fh_session_destroy(fh_session* s) {
   dev_free(s->x); dev_free(s->x2); dev_free(s->xn); dev_free(s->qkv); dev_free(s->o); dev_free(s->h);
   dev_free(s->part); dev_free(s->apart); dev_free(s->logits); dev_free(s->work);
   dev_free(s->step); dev_free(s->done); dev_free(s->out_counts); dev_free(s->gsplit);
+  if (s->hstage) (void)hipHostFree(s->hstage);
+  s->hstage = nullptr;
   dev_free(s->tokens); dev_free(s->out_ids); dev_free(s->uniforms); dev_free(s->dump);
   fh_context* c = s->ctx;
   const bool counted = s->counted;
@@ -1305,6 +1343,50 @@ int fh_forward_last(fh_session* s, const int32_t* ids, int batch, int T, float* 
   return check_split_error(s);
 }
 
+// Captures the per-step graphs the generation in s->gen needs (the decode step
+// unless the persistent kernel runs the cached steps, and the re-prefill once the
+// window slides) and sets the session's route.
+static int gen_capture(fh_session* s) {
+  GenState& g = s->gen;
+  const int C = s->d.context_length;
+  const fh_sampling* opts = &g.opts;
+  // dump/uniform pointers are baked into the graphs
+  float* saved_dump = s->dump;
+  double* saved_u = s->uniforms;
+  if (!g.dump) s->dump = nullptr;
+  if (!g.sampled) s->uniforms = nullptr;
+  GraphKey key;
+  key.B = g.B;
+  key.P = g.P;
+  key.max_new = g.max_new;
+  key.top_k = opts->top_k;
+  key.ngram = opts->no_repeat_ngram;
+  key.eos = opts->eos_id;
+  key.temperature = opts->temperature;
+  key.penalty = opts->repetition_penalty;
+  key.dump = s->dump;
+  key.uniforms = s->uniforms;
+  key.gen = s->buf_gen;
+  key.fused = s->use_fast();
+  int rc = FH_OK;
+  if (g.n_dec > 0 && !g.persistent) {
+    GraphKey k = key;
+    k.kind = 0;
+    rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, g.plan); });
+  }
+  if (rc == FH_OK && g.n_re > 0) {
+    GraphKey k = key;
+    k.kind = 1;
+    rc = capture(s, s->g_reprefill, k, [&] { return enqueue_window(s, C, g.plan); });
+  }
+  s->dump = saved_dump;
+  s->uniforms = saved_u;
+  if (rc != FH_OK) return rc;
+  s->route = g.persistent ? (FH_ROUTE_FUSED_STEP | (g.persist_sampled ? FH_ROUTE_FUSED_SAMPLER : 0))
+                          : (g.n_dec > 0 ? s->g_decode.route : 0);
+  return FH_OK;
+}
+
 // Validation (Sampler.cs:82-89, 169-175), buffers, prompt upload and the step
 // graphs of a generation; nothing is enqueued yet.  The state lives in s->gen.
 static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, int max_new, const fh_sampling* opts,
@@ -1356,24 +1438,6 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
   g.plan.max_new = max_new;
   g.plan.tok_stride = stride;
   g.plan.opts = &g.opts;
-  // dump/uniform pointers are baked into the graphs
-  float* saved_dump = s->dump;
-  double* saved_u = s->uniforms;
-  if (!dump) s->dump = nullptr;
-  if (!sampled) s->uniforms = nullptr;
-  GraphKey key;
-  key.B = B;
-  key.P = P;
-  key.max_new = max_new;
-  key.top_k = opts->top_k;
-  key.ngram = opts->no_repeat_ngram;
-  key.eos = opts->eos_id;
-  key.temperature = opts->temperature;
-  key.penalty = opts->repetition_penalty;
-  key.dump = s->dump;
-  key.uniforms = s->uniforms;
-  key.gen = s->buf_gen;
-  key.fused = s->use_fast();
   int rc = FH_OK;
   // which of steps 1..max_new-1 are cached decode steps (window fits) vs re-prefills
   for (int n = 1; n < max_new; n++) (P + n > C ? g.n_re : g.n_dec)++;
@@ -1381,28 +1445,22 @@ static int gen_setup(fh_session* s, const int32_t* prompts, int batch, int P, in
     rc = set_err(FH_ERR_HIP, "resetting the fused decode state failed");
   // greedy on the fused kernel: launches run whole runs of cached steps (the
   // argmax of a step feeds the next inside the kernel); otherwise one graph per step
-  g.persistent = g.n_dec > 0 && fused_greedy(s, opts);
-  // sampled with top-k (fh_generate only): the persistent launches draw in-kernel too
-  if (!g.persistent && one_shot && !s->no_sampled_fused && g.n_dec > 0 && s->use_fast() && sampled && !dump &&
+  {
+    float* saved_dump = s->dump;  // fused_greedy reads the dump pointer the graphs would bake in
+    if (!dump) s->dump = nullptr;
+    g.persistent = g.n_dec > 0 && fused_greedy(s, opts);
+    s->dump = saved_dump;
+  }
+  // sampled with top-k: the persistent launches draw in-kernel too (a stream's
+  // launch covers the steps of one fh_generate_next call, whose uniforms are on
+  // the device by then)
+  if (!g.persistent && !s->no_sampled_fused && g.n_dec > 0 && s->use_fast() && sampled && !dump &&
       s->fast.sampler_fits(opts->top_k, P + g.n_dec)) {
     g.persistent = true;
     g.persist_sampled = true;
   }
-  if (rc == FH_OK && g.n_dec > 0 && !g.persistent) {
-    GraphKey k = key;
-    k.kind = 0;
-    rc = capture(s, s->g_decode, k, [&] { return enqueue_decode(s, g.plan); });
-  }
-  if (rc == FH_OK && g.n_re > 0) {
-    GraphKey k = key;
-    k.kind = 1;
-    rc = capture(s, s->g_reprefill, k, [&] { return enqueue_window(s, C, g.plan); });
-  }
-  s->dump = saved_dump;
-  s->uniforms = saved_u;
+  if (rc == FH_OK) rc = gen_capture(s);
   if (rc != FH_OK) return rc;
-  s->route = g.persistent ? (FH_ROUTE_FUSED_STEP | (g.persist_sampled ? FH_ROUTE_FUSED_SAMPLER : 0))
-                          : (g.n_dec > 0 ? s->g_decode.route : 0);
   g.active = true;
   return FH_OK;
 }
@@ -1443,26 +1501,53 @@ static int gen_advance(fh_session* s, int upto) {
 }
 
 // Copies the ids (and logits) produced so far and checks the fused kernel's
-// hand-off status; synchronizes the stream.
+// hand-off status and the split-K GEMM's error word: every copy is queued on the
+// stream into pinned host memory, then one synchronization.
 static int gen_collect(fh_session* s, int32_t* out_ids, int32_t* out_counts, float* logits_dump) {
   GenState& g = s->gen;
   hipStream_t st = s->ctx->stream;
   const int B = g.B, V = s->d.vocab_size;
-  HIP_TRY(hipMemcpyAsync(out_ids, s->out_ids, sizeof(int32_t) * B * g.max_new, hipMemcpyDeviceToHost, st));
-  HIP_TRY(hipMemcpyAsync(out_counts, s->out_counts, sizeof(int32_t) * B, hipMemcpyDeviceToHost, st));
+  const size_t nid = (size_t)B * g.max_new, need = nid + B + 2;
+  if (need > s->hstage_cap) {
+    if (s->hstage) (void)hipHostFree(s->hstage);
+    s->hstage = nullptr;
+    s->hstage_cap = 0;
+    HIP_TRY(hipHostMalloc((void**)&s->hstage, need * sizeof(int32_t), hipHostMallocDefault));
+    s->hstage_cap = need;
+  }
+  int32_t* h_ids = s->hstage;
+  int32_t* h_counts = s->hstage + nid;
+  int32_t* h_err = h_counts + B;  // [0] fused kernel, [1] split-K GEMM
+  const bool fused = s->use_fast() && g.n_dec > 0;
+  h_err[0] = h_err[1] = 0;
+  HIP_TRY(hipMemcpyAsync(h_ids, s->out_ids, sizeof(int32_t) * nid, hipMemcpyDeviceToHost, st));
+  HIP_TRY(hipMemcpyAsync(h_counts, s->out_counts, sizeof(int32_t) * B, hipMemcpyDeviceToHost, st));
+  if (fused) HIP_TRY(hipMemcpyAsync(h_err, s->fast.error_word(), sizeof(int32_t), hipMemcpyDeviceToHost, st));
+  if (s->gsplit)
+    HIP_TRY(hipMemcpyAsync(h_err + 1, s->gsplit + s->gsplit_cap, sizeof(int32_t), hipMemcpyDeviceToHost, st));
   if (logits_dump)
     HIP_TRY(hipMemcpyAsync(logits_dump, s->dump, sizeof(float) * B * g.max_new * V, hipMemcpyDeviceToHost, st));
   HIP_TRY(hipStreamSynchronize(st));
-  if (check_split_error(s) != FH_OK) {
+  std::memcpy(out_ids, h_ids, sizeof(int32_t) * nid);
+  std::memcpy(out_counts, h_counts, sizeof(int32_t) * B);
+  if (h_err[1] != 0 && check_split_error(s) != FH_OK) {
     g.active = false;
     return FH_ERR_HIP;
   }
-  unsigned wait_code = 0;
-  if (s->use_fast() && g.n_dec > 0 && s->fast.check_error(&wait_code) != FH_OK) {
+  const unsigned wait_code = (unsigned)h_err[0];
+  if (fused && wait_code != 0) {
     s->fast.reset();
-    g.active = false;
     const unsigned what = (wait_code >> 24) & 0x7f;
-    if (what == 13 && g.persist_sampled) return kRetryPerStep;  // fh_generate repeats it on the per-step path
+    if (what == 13 && g.persist_sampled) {
+      // an exact top-k tie (or a non-finite logit): fh_generate repeats the
+      // generation per step; a stream resumes on the per-step sampler
+      if (g.one_shot) {
+        g.active = false;
+        return kRetryPerStep;
+      }
+      return kResumePerStep;
+    }
+    g.active = false;
     if (what == 11)
       return set_err(FH_ERR_HIP, "fused decode step: a token id outside [0, VocabSize) (results discarded)");
     if (what == 12)
@@ -1572,7 +1657,29 @@ int fh_generate_next(fh_session* s, int steps, const double* uniforms, int32_t* 
     (void)hipStreamSynchronize(s->ctx->stream);
     return rc;
   }
-  FH_TRY(gen_collect(s, out_ids, out_counts, nullptr));
+  rc = gen_collect(s, out_ids, out_counts, nullptr);
+  if (rc == kResumePerStep) {
+    // The in-kernel sampler met an exact tie at a top-k threshold (or a
+    // non-finite logit) in this call's steps.  Every earlier step it drew equals
+    // the per-step sampler's draw, so the stream goes on from a re-run of steps
+    // 0 .. next-1 on the per-step path (the uniforms of every step so far are on
+    // the device); ids already handed out are reproduced.
+    const int upto = g.next;
+    g.persistent = g.persist_sampled = false;
+    FH_TRY(reset_step_state(s));
+    if ((rc = gen_capture(s)) != FH_OK) {
+      g.active = false;
+      return rc;
+    }
+    g.next = 0;
+    rc = gen_advance(s, upto);
+    if (rc == FH_OK) rc = gen_collect(s, out_ids, out_counts, nullptr);
+    s->route |= FH_ROUTE_RETRIED;
+  }
+  if (rc != FH_OK) {
+    g.active = false;
+    return rc;
+  }
   *produced = g.next;
   if (g.next >= g.max_new) g.active = false;
   return FH_OK;

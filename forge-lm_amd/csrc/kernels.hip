@@ -1330,6 +1330,53 @@ __global__ void k_copy_bytes(const uint4* __restrict__ src, uint4* __restrict__ 
   if (blockIdx.x == 0 && (int)threadIdx.x < tail) dst_tail[threadIdx.x] = src_tail[threadIdx.x];
 }
 
+// Sum of the 32-bit words of a buffer (mod 2^64): per-block partials.  Block b
+// reads one contiguous chunk of the buffer (consecutive 4 KB per pass, eight
+// 16-byte loads in flight per thread), so the kernel streams the buffer at the
+// device's read bandwidth; integer addition makes the order immaterial.
+__global__ __launch_bounds__(256) void k_checksum_part(const uint4* __restrict__ src, size_t n16,
+                                                       const unsigned* __restrict__ tail, int ntail,
+                                                       unsigned long long* __restrict__ part) {
+  __shared__ unsigned long long red[256];
+  const size_t per = (n16 + gridDim.x - 1) / gridDim.x;
+  const size_t b0 = (size_t)blockIdx.x * per, b1 = b0 + per < n16 ? b0 + per : n16;
+  unsigned long long s = 0;
+  size_t i = b0 + threadIdx.x;
+  for (; i + 7 * 256 < b1; i += 8 * 256) {
+    uint4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = src[i + u * 256];
+#pragma unroll
+    for (int u = 0; u < 8; u++) s += (unsigned long long)v[u].x + v[u].y + v[u].z + v[u].w;
+  }
+  for (; i < b1; i += 256) {
+    const uint4 a = src[i];
+    s += (unsigned long long)a.x + a.y + a.z + a.w;
+  }
+  if (blockIdx.x == 0 && (int)threadIdx.x < ntail) s += tail[threadIdx.x];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+__global__ __launch_bounds__(256) void k_checksum_final(const unsigned long long* __restrict__ part, int n,
+                                                        unsigned long long* __restrict__ out) {
+  __shared__ unsigned long long red[256];
+  unsigned long long s = 0;
+  for (int i = threadIdx.x; i < n; i += 256) s += part[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if ((int)threadIdx.x < o) red[threadIdx.x] += red[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[0] = red[0];
+}
+
 // out[i] = bf16(in[i]), nearest-even, over a grid-stride loop
 __global__ void k_round_bf16(const float* __restrict__ in, bf16_t* __restrict__ out, size_t n) {
   const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -1501,6 +1548,19 @@ hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes)
   hipLaunchKernelGGL(k_copy_bytes, dim3(blocks), dim3(256), 0, st, static_cast<const uint4*>(src),
                      static_cast<uint4*>(dst), n16, static_cast<const unsigned char*>(src) + n16 * 16,
                      static_cast<unsigned char*>(dst) + n16 * 16, tail);
+  return hipGetLastError();
+}
+
+hipError_t launch_checksum(hipStream_t st, const void* src, size_t bytes, unsigned long long* part, int nparts,
+                           unsigned long long* out, hipEvent_t read_done) {
+  FH_CHECK_ARG(src && part && out && nparts >= 1 && nparts <= kChecksumParts && ((uintptr_t)src % 16) == 0 &&
+               bytes % 4 == 0);
+  const size_t n16 = bytes / 16;
+  const int ntail = (int)((bytes % 16) / 4);
+  hipLaunchKernelGGL(k_checksum_part, dim3(nparts), dim3(256), 0, st, static_cast<const uint4*>(src), n16,
+                     reinterpret_cast<const unsigned*>(static_cast<const char*>(src) + n16 * 16), ntail, part);
+  if (read_done) (void)hipEventRecord(read_done, st);
+  hipLaunchKernelGGL(k_checksum_final, dim3(1), dim3(256), 0, st, part, nparts, out);
   return hipGetLastError();
 }
 

@@ -180,6 +180,12 @@ hipError_t launch_round_bf16(hipStream_t st, const float* in, size_t n, bf16_t* 
 
 // dst[0..bytes) = src[0..bytes) on the device (both 16-byte aligned).
 hipError_t launch_copy(hipStream_t st, void* dst, const void* src, size_t bytes);
+// Sum of the 32-bit words of src (bytes % 4 == 0, 16-byte aligned) mod 2^64 into
+// *out (device); part holds nparts (<= kChecksumParts) per-block partials;
+// read_done (optional) is recorded after the pass that reads src.
+constexpr int kChecksumParts = 4096;
+hipError_t launch_checksum(hipStream_t st, const void* src, size_t bytes, unsigned long long* part, int nparts,
+                           unsigned long long* out, hipEvent_t read_done);
 
 struct SampleArgs {
   const float* logits;  // [B][V] raw ForwardLast logits

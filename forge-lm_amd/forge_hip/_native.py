@@ -31,7 +31,7 @@ FH_ROUTE_FUSED_SAMPLER, FH_ROUTE_RETRIED, FH_ROUTE_FALLBACK = 16, 32, 64
 EXPORTS = (
     "fh_last_error", "fh_version", "fh_random_doubles", "fh_context_create", "fh_context_destroy",
     "fh_context_info", "fh_context_memory", "fh_buffer_alloc", "fh_buffer_free", "fh_buffer_write", "fh_buffer_read",
-    "fh_buffer_copy", "fh_matmul_nn",
+    "fh_buffer_copy", "fh_buffer_checksum", "fh_matmul_nn",
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_init_weights", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
     "fh_generate", "fh_last_timing", "fh_last_route", "fh_sample_logits", "fh_sample_logits_noalloc",
@@ -103,6 +103,7 @@ def lib():
     L.fh_context_memory.argtypes = [vp, P(ctypes.c_uint64), P(ctypes.c_uint64)]
     L.fh_buffer_alloc.argtypes = [vp, ctypes.c_size_t, P(vp)]
     L.fh_buffer_free.argtypes = [vp, vp]
+    L.fh_buffer_checksum.argtypes = [vp, vp, ctypes.c_size_t, P(ctypes.c_uint64), P(f32)]
     L.fh_buffer_write.argtypes = [vp, vp, vp, ctypes.c_size_t]
     L.fh_buffer_read.argtypes = [vp, vp, vp, ctypes.c_size_t]
     L.fh_buffer_copy.argtypes = [vp, vp, vp, ctypes.c_size_t, P(ctypes.c_float)]

@@ -113,6 +113,12 @@ int fh_buffer_read(fh_context* ctx, void* dst, const void* src_dev, size_t bytes
  * ms_out is not NULL it receives the kernel's duration from HIP events (the
  * bandwidth calibration of the benchmark's traffic counters). */
 int fh_buffer_copy(fh_context* ctx, void* dst_dev, const void* src_dev, size_t bytes, float* ms_out);
+/* The sum of a device buffer's 32-bit words mod 2^64 (an integrity check of an
+ * upload; no reference counterpart), synchronous.  src 16-byte aligned, bytes a
+ * multiple of 4.  When ms_out is not NULL it receives the duration of the pass
+ * that reads the buffer (one read of every byte: the device's read bandwidth,
+ * reported next to the decode kernel's roofline). */
+int fh_buffer_checksum(fh_context* ctx, const void* src_dev, size_t bytes, uint64_t* sum_out, float* ms_out);
 
 /* ITensorBackend.MatMulNN(a, b, y, M, K, N, accumulate) (ITensorBackend.cs:22) on
  * device buffers: y[M][N] = a[M][K] @ b[K][N], or += when accumulate != 0.  a and

@@ -289,8 +289,11 @@ def decision_gaps(adj, T, k, u):
     return gap_k, float(min(hi - target, target - lo) / cum[-1])
 
 
-def test_c3_sampling_path(fhp, oracle, backend):
-    """T 0.7, top-k 30, repetition 1.1, no-repeat-ngram 4, prompt 32 + 512.
+@pytest.mark.parametrize("params", ["init", "trained"])
+def test_c3_sampling_path(fhp, oracle, backend, params):
+    """T 0.7, top-k 30, repetition 1.1, no-repeat-ngram 4, prompt 32 + 512,
+    at the initial parameters and at trained-like ones (LayerNorm and bias values away
+    from their (1, 0, 0) starting points).
 
     1. Every step: the oracle's sampler on the GPU's logits, the GPU's window and the
        same uniform returns the GPU's id (the sampler is exact).
@@ -307,7 +310,7 @@ def test_c3_sampling_path(fhp, oracle, backend):
     """
     shape = (16384, 1024, 768, 12, 12)
     T, K, PEN, NG = 0.7, 30, 1.1, 4
-    m, oc, w = make_model(fhp, oracle, backend, shape, 1234, trained=False)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234, trained=params == "trained")
     prompt = fhp.TrainingRandom(42).ids(16384, 32)
     u = fhp.Random(1).next_doubles(512)
     ids, lg = fhp.Sampler.generate(m, prompt, 512, T, K, fhp.Random(1), repetition_penalty=PEN,
@@ -332,7 +335,7 @@ def test_c3_sampling_path(fhp, oracle, backend):
             assert gk <= 2 * d or gc <= 4 * d, (n, gk, gc, d)
             flips.append(n)
     agree = 512 - len(flips)
-    print(f"C3: the oracle's decision on its own logits equals the GPU's id at {agree}/512 steps "
+    print(f"C3 ({params}): the oracle's decision on its own logits equals the GPU's id at {agree}/512 steps "
           f"(flips within the fp32 tolerance at {flips})", flush=True)
     assert agree >= 504, f"only {agree}/512 steps agree; flips at {flips}"
     # the same generation without the logits dump draws inside the persistent kernel:
@@ -344,7 +347,7 @@ def test_c3_sampling_path(fhp, oracle, backend):
     rids, rlg = oracle.generate(oc, w, prompt, 512, temperature=T, top_k=K, uniforms=u, penalty=PEN, ngram=NG,
                                 return_logits=True)
     same = int(np.argmax(ids != rids)) if np.any(ids != rids) else 512
-    print(f"C3: free-running GPU and oracle trajectories agree for {same}/512 steps", flush=True)
+    print(f"C3 ({params}): free-running GPU and oracle trajectories agree for {same}/512 steps", flush=True)
     assert same == 512 or same in flips, f"the trajectories part at step {same}, not at a tolerance flip {flips}"
     m.dispose()
 
@@ -443,6 +446,19 @@ def test_bf16_operand_rounding_is_nearest_even_bit_for_bit(fhp, backend):
     assert np.array_equal(got, want), int(np.sum(got != want))
     for buf in (bufa, bufb, bufy):
         buf.free()
+
+
+@pytest.mark.parametrize("nbytes", [4, 60, 4096, 1 << 20, (64 << 20) + 52])
+def test_buffer_checksum(fhp, backend, nbytes):
+    # fh_buffer_checksum: the sum of the buffer's 32-bit words mod 2^64 (tail words
+    # past the last 16-byte unit included), against numpy
+    r = np.random.default_rng(nbytes)
+    words = r.integers(0, 2**32, size=nbytes // 4, dtype=np.uint64).astype(np.uint32)
+    buf = fhp.DeviceBuffer.from_array(backend, words)
+    got, ms = buf.checksum(nbytes)
+    assert got == int(np.sum(words, dtype=np.uint64))  # numpy's uint64 sum wraps mod 2^64
+    assert ms >= 0
+    buf.free()
 
 
 @pytest.mark.parametrize("M,K,N", [(2000, 512, 4000), (256, 4096, 1024), (8192, 1024, 256)])
@@ -562,11 +578,12 @@ def test_c5_shape_bf16_generate_matches_oracle(fhp, oracle, backend):
 def test_c5_shape_bf16_window_path_matches_oracle(fhp, oracle, backend, B, P):
     # 256 window rows or more in a bf16 session: LayerNorm, attention and GELU write
     # bf16 operands for the bf16 GEMM (B*P = 256 uses 128-row tiles, 8192 the
-    # 256-row tiles of the full C5 prefill; P = 1024 fills the window, so the second
-    # token re-prefills it).  Checked against the oracle on bf16-rounded parameters
-    # (2e-2) for the first and last sequence, and against the fp32-operand path
+    # 256-row tiles of the full C5 prefill; P = 1024 fills the window, so every token
+    # after the first re-prefills it: 4 steps there).  Checked against the oracle on
+    # bf16-rounded parameters (2e-2) at every step for the first and last sequence,
+    # and against the fp32-operand path
     shape = (16384, 1024, 1024, 16, 16)
-    NEW = 2
+    NEW = 4 if P == 1024 else 2
     ocfg = oracle.Config(*shape)
     w = oracle.trained_like(ocfg, oracle.init_weights(ocfg, 1234), 2234)
     wr = bf16_round(w)[0]
@@ -584,16 +601,22 @@ def test_c5_shape_bf16_window_path_matches_oracle(fhp, oracle, backend, B, P):
     ids2, lg2 = fhp.Sampler.generate(m2, prompts, NEW, 0.0, 0, None, return_logits=True)
     m2.dispose()
     oracle.set_threads(16)
+    C = shape[1]
     for b in (0, B - 1):
         # the two paths round the same operands to bf16 but sum in different orders
         # (split K in the fp32-operand GEMM); 16 layers of bf16 rounding carry that
         # to about 1e-2 of the logits, inside the bf16 bar
         assert rel_err(lg[b][0], lg2[b][0]) <= 2e-2
-        rids, rlg = oracle.generate(ocfg, wr, prompts[b], NEW, return_logits=True)
-        assert rel_err(lg[b], rlg) <= 2e-2
-        top2 = np.sort(rlg[0])[-2:]
-        if top2[1] - top2[0] > 4e-2:
-            assert ids[b][0] == rids[0]
+        # every step teacher-forced on the GPU's own window (after the first step the
+        # window slides: the last C ids of prompt + ids so far, positions from 0),
+        # so a step after a near tie is still compared on the same input
+        for n in range(NEW):
+            window = np.concatenate([prompts[b], ids[b][:n]]).astype(np.int32)[-C:]
+            ref = oracle.forward(ocfg, wr, window)[-1]
+            assert rel_err(lg[b][n], ref) <= 2e-2, (b, n)
+            top2 = np.sort(ref)[-2:]
+            if top2[1] - top2[0] > 4e-2:
+                assert ids[b][n] == int(np.argmax(ref)), (b, n)
 
 
 @pytest.mark.parametrize("case", ["greedy_c2", "sampled", "slides", "eos"])
@@ -625,6 +648,79 @@ def test_generate_stream_matches_one_shot(fhp, oracle, backend, case):
         assert got == want, (case, chunk)
     if case == "eos":
         assert len(want) <= 10 and want[-1] == kw["eos_id"]
+    m.dispose()
+
+
+def _session_route(fhp, m):
+    import ctypes
+    r = ctypes.c_int32()
+    fhp._native.check(fhp._native.lib().fh_last_route(m.handle, ctypes.byref(r)))
+    return r.value
+
+
+def _stream_deferred(fhp, m, prompt, new, opts, u, chunk):
+    """fh_generate_begin without uniforms, then fh_generate_next calls of `chunk` steps,
+    each bringing its steps' uniforms (as the C# binding draws them); stops at EOS."""
+    import ctypes
+    N = fhp._native
+    prompt = np.ascontiguousarray(prompt, np.int32)
+    N.check(N.lib().fh_generate_begin(m.handle, prompt.ctypes.data, 1, prompt.size, new, ctypes.byref(opts), None))
+    out = np.zeros(new, np.int32)
+    counts = np.zeros(1, np.int32)
+    produced = ctypes.c_int32()
+    done = 0
+    while done < new:
+        buf = np.zeros(chunk, np.float64)
+        part = u[done:done + chunk]
+        buf[:part.size] = part
+        N.check(N.lib().fh_generate_next(m.handle, chunk, buf.ctypes.data, out.ctypes.data, counts.ctypes.data,
+                                         ctypes.byref(produced)))
+        done = produced.value
+        if counts[0] < done:  # EOS
+            break
+    return list(out[:counts[0]])
+
+
+@pytest.mark.parametrize("chunk", [1, 16])
+def test_sampled_stream_runs_the_in_kernel_sampler(fhp, oracle, backend, chunk):
+    """The CLI's defaults (T 0.8, top-k 40, an EOS id set, Program.cs:642-644) streamed
+    through fh_generate_next with each call's uniforms: on the fused path every call's
+    steps run as one launch of the persistent sampled kernel (one step per call with
+    chunk 1), and the ids equal one fh_generate call's, EOS included."""
+    N = fhp._native
+    shape = (16384, 1024, 768, 2, 12)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 81)
+    prompt = fhp.TrainingRandom(19).ids(shape[0], 40)
+    new = 70
+    u = fhp.Random(1).next_doubles(new)
+    full = list(fhp.Sampler.generate(m, prompt, new, 0.8, 40, fhp.Random(1)))
+    eos = int(full[50])  # stops the stream at its first occurrence
+    want = list(fhp.Sampler.generate(m, prompt, new, 0.8, 40, fhp.Random(1), eos_id=eos))
+    assert route(fhp) & N.FH_ROUTE_FUSED_SAMPLER
+    assert want[-1] == eos and len(want) <= 51
+    got = _stream_deferred(fhp, m, prompt, new, N.Sampling(0.8, 40, 1.0, 0, eos, 0), u, chunk)
+    assert _session_route(fhp, m) & N.FH_ROUTE_FUSED_SAMPLER
+    assert got == want
+    m.dispose()
+
+
+def test_sampled_stream_resumes_per_step_after_a_tie(fhp, oracle, backend):
+    """An all-ties model (tok_emb zero: every logit is 0) makes the in-kernel sampler
+    meet an exact tie at its top-k threshold in a stream: the stream re-runs its steps
+    on the per-step sampler and goes on (FH_ROUTE_RETRIED); ids equal fh_generate's."""
+    N = fhp._native
+    shape = (16384, 1024, 768, 2, 12)
+    oc = oracle.Config(*shape)
+    w = oracle.trained_like(oc, oracle.init_weights(oc, 3), 4)
+    oracle.params(oc, w)["tok_emb"][...] = 0
+    m = fhp.GptModel(fhp.ModelConfig(*shape), backend)
+    m.load_weights(w)
+    prompt = fhp.TrainingRandom(2).ids(shape[0], 20)
+    want = list(fhp.Sampler.generate(m, prompt, 30, 0.9, 20, fhp.Random(8), repetition_penalty=1.3))
+    u = fhp.Random(8).next_doubles(30)
+    got = _stream_deferred(fhp, m, prompt, 30, N.Sampling(0.9, 20, 1.3, 0, -1, 0), u, 7)
+    assert _session_route(fhp, m) & N.FH_ROUTE_RETRIED
+    assert got == want
     m.dispose()
 
 
@@ -842,9 +938,11 @@ def test_batched_decode_attention_in_proj_over_four_chunks(fhp, oracle, backend,
     m.dispose()
 
 
-def test_c4_config_batch32_long_context(fhp, oracle, backend):
+@pytest.mark.parametrize("params", ["init", "trained"])
+def test_c4_config_batch32_long_context(fhp, oracle, backend, params):
     """BASELINE config 4 at its full size: 32 sequences of 512 PCG32 prompt ids (seeds
-    42 + b), 512 greedy steps each, so the windows run from 513 to 1023 keys.
+    42 + b), 512 greedy steps each, so the windows run from 513 to 1023 keys; at the
+    initial parameters and at trained-like ones.
 
     * every sequence's ids equal the same prompt decoded alone (batch 1, the fused
       step), up to a step where the two runs part at a near tie of the batched run's
@@ -856,7 +954,7 @@ def test_c4_config_batch32_long_context(fhp, oracle, backend):
     """
     shape = (16384, 1024, 768, 12, 12)
     B, P, NEW = 32, 512, 512
-    m, oc, w = make_model(fhp, oracle, backend, shape, 1234, batch=B, trained=False)
+    m, oc, w = make_model(fhp, oracle, backend, shape, 1234, batch=B, trained=params == "trained")
     prompts = np.stack([fhp.TrainingRandom(42 + b).ids(shape[0], P) for b in range(B)])
     ids, lg = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
     assert route(fhp) & fhp._native.FH_ROUTE_ATTN_IN_PROJ
@@ -874,7 +972,7 @@ def test_c4_config_batch32_long_context(fhp, oracle, backend):
             assert gap <= 2 * TOL_F32 * max(1.0, float(row.max())), (b, n, gap)
             parted.append((b, n))
     single.dispose()
-    print(f"C4: {B - len(parted)}/{B} sequences equal their batch-1 decode over all 512 steps; "
+    print(f"C4 ({params}): {B - len(parted)}/{B} sequences equal their batch-1 decode over all 512 steps; "
           f"near-tie partings at {parted}", flush=True)
     oracle.set_threads(16)
     for b in (0, B - 1):
