@@ -1685,8 +1685,8 @@ int fh_generate_next(fh_session* s, int steps, const double* uniforms, int32_t* 
   return FH_OK;
 }
 
-// Debug helper (not part of the public header): per-block timestamps (256 x 32)
-// of the last fused decode step when the session was created with FORGE_HIP_TRACE=1.
+// Per-block timestamps (256 x 64) of one traced step of the last fused decode
+// launch when the session was created with FORGE_HIP_TRACE=1.
 int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n) {
   if (!s || !out || n < 0) return set_err(FH_ERR_INVALID, "bad argument");
   if (!s->fast.trace) return set_err(FH_ERR_STATE, "tracing is off (set FORGE_HIP_TRACE=1 before creating the session)");

@@ -34,7 +34,7 @@ EXPORTS = (
     "fh_buffer_copy", "fh_buffer_checksum", "fh_matmul_nn",
     "fh_session_create", "fh_session_destroy", "fh_param_count", "fh_param_info",
     "fh_session_init_random", "fh_init_weights", "fh_session_load_weights", "fh_session_read_param", "fh_forward_last",
-    "fh_generate", "fh_last_timing", "fh_last_route", "fh_sample_logits", "fh_sample_logits_noalloc",
+    "fh_generate", "fh_last_timing", "fh_last_route", "fh_debug_fused_trace", "fh_sample_logits", "fh_sample_logits_noalloc",
     "fh_checkpoint_info", "fh_session_load_checkpoint", "fh_sha256", "fh_generate_begin", "fh_generate_next",
     # op-level ITensorBackend
     "fh_op_matmul_nn", "fh_op_matmul_nt", "fh_op_matmul_tn", "fh_op_pack_heads", "fh_op_unpack_heads",
@@ -121,6 +121,7 @@ def lib():
     L.fh_generate.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, P(Sampling), vp, vp, vp, vp]
     L.fh_last_timing.argtypes = [vp, P(f64), P(f64), P(i32), P(i32)]
     L.fh_last_route.argtypes = [vp, P(i32)]
+    L.fh_debug_fused_trace.argtypes = [vp, vp, ctypes.c_int]
     L.fh_sample_logits.argtypes = [vp, vp, ctypes.c_int, vp, ctypes.c_int, P(Sampling), f64, P(i32)]
     L.fh_sample_logits_noalloc.argtypes = L.fh_sample_logits.argtypes
     L.fh_checkpoint_info.argtypes = [ctypes.c_char_p, P(ModelDesc), ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int]

@@ -208,6 +208,14 @@ int fh_last_timing(fh_session* s, double* prefill_ms, double* decode_ms, int32_t
                                        on the generic kernels, whose ids it returned */
 int fh_last_route(fh_session* s, int32_t* route);
 
+/* Diagnostics of the persistent decode kernel (no reference counterpart): with
+ * FORGE_HIP_TRACE=1 set when the session is created, each fused launch records
+ * wall-clock timestamps (100 MHz) of one step (layer 1 of its sixth token, and the
+ * head of that token) in every block: 64 per block, block-major, n >= 256 * 64.
+ * Entries 0-31 are the control wave's marks, 32-63 data wave 0's; entry 12 is the
+ * block's XCD.  forge_hip.trace prints the per-hand-off timeline from them. */
+int fh_debug_fused_trace(fh_session* s, unsigned long long* out, int n);
+
 /* Sampler.ApplyRepetitionControls + Sampler.Sample on one logit row already on
  * the device: logits_dev [V] (not modified), history [n_hist] host ids, u01 the
  * NextDouble for this draw.  Returns the id in *out_id. */
