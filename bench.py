@@ -219,7 +219,7 @@ def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
     """(HBM bytes per launch of `kernel`, HBM / algorithmic bytes of `kernel`, what
     build they were counted on) from a committed counter summary (rocprofv3 --pmc
     runs; the counters cannot be read inside this run); None where it has none."""
-    value, ratio, build = None, None, None
+    value, ratio, build, where = None, None, None, None
     try:
         with open(os.path.join(ROOT, path)) as f:
             for line in f:
@@ -229,9 +229,11 @@ def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
                     ratio = float(line.split(":", 1)[1].split()[0])
                 elif line.startswith("measured_on:"):
                     build = line.split(":", 1)[1].strip()
+                elif line.startswith("counted_at:"):
+                    where = line.split(":", 1)[1].strip()
     except OSError:
         pass
-    return value, ratio, build
+    return value, ratio, (f"{build}, {where}" if where else build)
 
 
 def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: int = 0, prompt: int = 0,
@@ -337,8 +339,8 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
             if ratio is not None:
                 # the counted HBM / algorithmic ratio applied to this run's windows
                 traffic = int(ratio * step_bytes * tokens_per_launch)
-                traffic_src = (f"{TRAFFIC_PROFILE_C4}: HBM / algorithmic bytes {ratio:.4f} counted at windows "
-                               f"513..575 ({build}), times this run's algorithmic bytes")
+                traffic_src = (f"{TRAFFIC_PROFILE_C4}: HBM / algorithmic bytes {ratio:.4f} ({build}), times this "
+                               f"run's algorithmic bytes")
         out.update({
             "decode_tok_s": round(B * n_dec / dec_s, 2),
             "decode_us_per_step": round(avg_step_s * 1e6, 2),
