@@ -231,6 +231,8 @@ def profiled_traffic(kernel: str, path: str = TRAFFIC_PROFILE):
                     build = line.split(":", 1)[1].strip()
                 elif line.startswith("counted_at:"):
                     where = line.split(":", 1)[1].strip()
+                elif line.startswith("extra_bytes_per_step:") and kernel in line:
+                    value = int(line.split(":", 1)[1].split()[0])
     except OSError:
         pass
     return value, ratio, (f"{build}, {where}" if where else build)
@@ -335,12 +337,13 @@ def run_workload(name: str, args, steps: int, warmup: int, with_cpu: bool, new: 
             traffic, _, build = profiled_traffic(kernel, TRAFFIC_PROFILE_2)
             traffic_src = f"{TRAFFIC_PROFILE_2} (counted on {build})" if traffic is not None else None
         elif not persistent and name == "c4":
-            _, ratio, build = profiled_traffic(kernel, TRAFFIC_PROFILE_C4)
-            if ratio is not None:
-                # the counted HBM / algorithmic ratio applied to this run's windows
-                traffic = int(ratio * step_bytes * tokens_per_launch)
-                traffic_src = (f"{TRAFFIC_PROFILE_C4}: HBM / algorithmic bytes {ratio:.4f} ({build}), times this "
-                               f"run's algorithmic bytes")
+            extra, ratio, build = profiled_traffic(kernel, TRAFFIC_PROFILE_C4)
+            if extra is not None:
+                # the counted bytes above the algorithmic ones (split-K partial sums, which
+                # do not grow with the window) added to this run's algorithmic bytes
+                traffic = int((step_bytes + extra) * tokens_per_launch)
+                traffic_src = (f"{TRAFFIC_PROFILE_C4}: {extra / 1e9:.3f} GB per step above the algorithmic "
+                               f"bytes ({build}; ratio {ratio:.4f} there), added to this run's algorithmic bytes")
         out.update({
             "decode_tok_s": round(B * n_dec / dec_s, 2),
             "decode_us_per_step": round(avg_step_s * 1e6, 2),
