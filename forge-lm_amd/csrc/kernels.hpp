@@ -171,6 +171,14 @@ template <typename WT>
 hipError_t launch_gemm_mfma_split(hipStream_t st, const float* a, int M, int K, const WT* Wt, int N, float* part,
                                   size_t part_floats, int cus, int* splits, const AOperand* aop = nullptr);
 
+// Decode GEMMs of at most 32 fp32 rows (gemm_skinny.hip): 16 output columns per
+// block over a 768-deep K range, S = K / 768 blocks per column strip.  EPI_GELU
+// (S == 1): y = gelu(x @ W + bias) [M][N]; EPI_NONE: y = part[S][M][N] of x @ W
+// (no bias).  gemm_skinny_fits says whether a shape qualifies.
+bool gemm_skinny_fits(int M, int K, int N);
+hipError_t launch_gemm_skinny(hipStream_t st, const float* x, int M, int K, const float* Wt, int N,
+                              const float* bias, int epi, float* y, int* splits);
+
 // Wt[n][k] = W[k][n].
 template <typename WT>
 hipError_t launch_transpose(hipStream_t st, const WT* W, int K, int N, WT* Wt);
