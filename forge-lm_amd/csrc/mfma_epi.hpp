@@ -25,12 +25,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const void* base, si
 }
 
 // GELU for an output rounded to bf16 (relative step 2^-8): 0.5 v (1 + tanh u) =
-// v / (1 + e^(-2u)) on the hardware exp and reciprocal, a few fp32 ulps from the
-// tanhf form, far below the rounding that follows
+// v / (1 + 2^(-2 u log2 e)) on the hardware exp2 and reciprocal, with
+// -2 u log2 e = v (K0 + K1 v^2) (C = MathF.Sqrt(2f / MathF.PI), 0.044715 and
+// log2 e folded into two constants: 5 VALU operations and 2 transcendentals per
+// element, where the epilogue of a bf16-out GEMM tile is VALU-bound), a few fp32
+// ulps from the tanhf form, far below the rounding that follows
 __device__ __forceinline__ float gelu_for_bf16(float v) {
-  const float C = 0.7978845238685608f;  // MathF.Sqrt(2f / MathF.PI) in fp32
-  const float u = C * (v + 0.044715f * v * v * v);
-  return v * __builtin_amdgcn_rcpf(1.f + __expf(-2.f * u));
+  constexpr float K0 = (float)(-2.0 * 0.7978845238685608 * 1.4426950408889634);
+  constexpr float K1 = (float)(-2.0 * 0.7978845238685608 * 1.4426950408889634 * 0.044715);
+  const float q = v * __builtin_fmaf(v * v, K1, K0);
+  return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(q));
 }
 
 // rows trow0 + mfma_acc_row(lane, r) (relative to the resources' first row) of column col
