@@ -243,10 +243,11 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(const float* __restrict__ A, 
   if (col >= N) return;
   const int nrows = min(BM, M - m0);
   if (part) {
-    // split-K partial of this block's K chunk: raw sums, no bias or epilogue
+    // split-K partial of this block's K chunk: raw sums, no bias or epilogue (stored
+    // with the non-temporal hint: read once, by the reduction or the attention)
     const __amdgpu_buffer_rsrc_t rp = rows_rsrc(part, (size_t)blockIdx.z * M + m0, nrows, N, 4);
 #pragma unroll
-    for (int t = 0; t < MT; t++) mfma_store_tile<EPI_NONE, false, false>(acc[t], lane, t * 32, col, N, 0.f, rp, rp);
+    for (int t = 0; t < MT; t++) mfma_store_tile<EPI_NONE, false, false, 2>(acc[t], lane, t * 32, col, N, 0.f, rp, rp);
     return;
   }
   const float bcol = bias ? bias[col] : 0.f;

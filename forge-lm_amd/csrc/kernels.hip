@@ -171,7 +171,8 @@ __global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ 
   const bool on = c < N;
   // one column per thread, up to 32 of its partials in flight together through a
   // bounded resource (skipped ones, past S or N, read as zeros); the partials add
-  // in order, and the zeros after the last one change nothing
+  // in order, and the zeros after the last one change nothing.  Each partial is
+  // read once: the loads carry the non-temporal hint (C4: 870 -> 863 us per step).
   const int pbytes = (int)((size_t)S * M * N * 4);
   const __amdgpu_buffer_rsrc_t rp =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part), (short)0, pbytes, 0x00020000);
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(1024) void k_epilogue_ln(const float* __restrict__ 
 #pragma unroll
     for (int ii = 0; ii < 32; ii++) {
       const int off = (on && i0 + ii < S) ? (int)((((size_t)(i0 + ii) * M + r) * N + c) * 4) : pbytes;
-      t[ii] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
+      t[ii] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 2));
     }
 #pragma unroll
     for (int ii = 0; ii < 32; ii++) v += t[ii];

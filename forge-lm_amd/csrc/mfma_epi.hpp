@@ -37,8 +37,10 @@ __device__ __forceinline__ float gelu_for_bf16(float v) {
   return v * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(q));
 }
 
-// rows trow0 + mfma_acc_row(lane, r) (relative to the resources' first row) of column col
-template <int EPI, bool RES, bool OUT_BF16>
+// rows trow0 + mfma_acc_row(lane, r) (relative to the resources' first row) of column col;
+// SAUX is the fp32 stores' cache policy (2: non-temporal, for split-K partial sums,
+// which are read once by the kernel after: C4 859 -> 850-853 us per step)
+template <int EPI, bool RES, bool OUT_BF16, int SAUX = 0>
 __device__ __forceinline__ void mfma_store_tile(const mfma_f32x16_t& acc, int lane, int trow0, int col, int N,
                                                 float bcol, __amdgpu_buffer_rsrc_t rres,
                                                 __amdgpu_buffer_rsrc_t ry) {
@@ -58,7 +60,7 @@ __device__ __forceinline__ void mfma_store_tile(const mfma_f32x16_t& acc, int la
     if constexpr (OUT_BF16)
       __builtin_amdgcn_raw_buffer_store_b16(bf16_rn(s), ry, e * 2, 0, 0);
     else
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, s), ry, e * 4, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, s), ry, e * 4, 0, SAUX);
   }
 }
 
