@@ -41,7 +41,8 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(const float* __restrict__ x
   const int k0 = split * SK_KB + w * SK_KW;
   const int j = lane & 15, q = lane >> 4;
   // bounded resources: A rows past M read as zeros (their sums are never stored);
-  // the block's 16 rows of W^T
+  // the block's 16 rows of W^T, read once per step: non-temporal hint (C4 835 ->
+  // 828 us per step)
   const __amdgpu_buffer_rsrc_t ra =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, M * K * 4, 0x00020000);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(const float* __restrict__ x
 #pragma unroll
   for (int t = 0; t < SK_T; t++) {
     const int k = k0 + 16 * t + 4 * q;
-    b[t] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, (j * K + k) * 4, 0, 0));
+    b[t] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rb, (j * K + k) * 4, 0, 2));
     a0[t] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, (j * K + k) * 4, 0, 0));
     a1[t] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ra, ((16 + j) * K + k) * 4, 0, 0));
   }
