@@ -1456,12 +1456,12 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
     __hip_atomic_fetch_add(p.launch, (unsigned)p.nsteps, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Data waves: weight tiles in registers.  Each tile is requested right after
-// the phase that consumed it, so it has a whole layer to arrive and a block
-// issues about one tile per phase (in-flight loads delay every hand-off read
-// of the CU, so they are spread evenly):
+// Data waves: weight tiles in registers.  A tile requested right after the
+// phase that consumed it has a whole layer to arrive, and a block then issues
+// about one tile per phase (in-flight loads delay every hand-off read of the CU,
+// so they are spread over the layer):
 //   A: rq(l+1)   B (attention blocks): K/V(l+1)   C: rp(l+1)   D: rf(l+1)   E: rm(l+1)
-// Every load is unconditional (an empty buffer resource past the last layer),
+// The sites below move some of them, by measurement.  Every load is unconditional (an empty buffer resource past the last layer),
 // so each register has one producer and one consumer per iteration.  After a
 // failed wait (sh.fail, read after each barrier) the stores are skipped.
 // Load sites of the data loop, in program order within a layer: after A's
@@ -1469,11 +1469,14 @@ __device__ __forceinline__ void ctrl_loop(const KParams& p, Lds<D, H>& sh, SampL
 // C, D and E.  A tile requested before its use in the layer is the layer's
 // own; after its use, the next layer's (the next token's first after the last).
 enum Site : int { S_AEND = 0, S_BSTART = 1, S_BEND = 2, S_CEND = 3, S_DEND = 4, S_EEND = 5 };
-// site of each tile: non-attention blocks request mlp.fc / mlp.proj / next qkv
-// right after A (their only slack is the attention window); attention blocks
-// spread theirs over the layer
+// site of each tile, by measurement (sweeps of every combination): non-attention
+// blocks request mlp.fc / mlp.proj right after A (their only slack is the
+// attention window) and the next layer's qkv after E; attention blocks request
+// their attn.proj tiles at the end of B, right before C, and spread the rest over
+// the layer (with the weight tiles' non-temporal hint these two sites measured
+// 136.3 against 140.3 us per token; the sampled kernel is unchanged by them)
 #ifndef FH_NQ
-#define FH_NQ S_AEND
+#define FH_NQ S_EEND
 #endif
 #ifndef FH_NP
 #define FH_NP S_CEND
@@ -1491,7 +1494,7 @@ enum Site : int { S_AEND = 0, S_BSTART = 1, S_BEND = 2, S_CEND = 3, S_DEND = 4, 
 #define FH_AKV S_BEND
 #endif
 #ifndef FH_AP
-#define FH_AP S_CEND
+#define FH_AP S_BEND
 #endif
 #ifndef FH_AF
 #define FH_AF S_DEND
