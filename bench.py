@@ -83,9 +83,16 @@ def decode_bytes_per_step(c, attended: float, batch: int = 1, esize: int = 4) ->
 
 
 def prefill_flops(c, T: int, batch: int) -> float:
-    """Algorithmic FLOPs of one prefill forward: the linear layers, causal QK^T and PV, the last-row head."""
+    """FLOPs of one bf16 prefill forward as the library runs it: layers 0..L-2 in
+    full (the linear layers, causal QK^T and PV over every row), the last layer's
+    qkv on every row (it fills the K/V caches) and the rest of it (attention of
+    the last query over T keys, attn.proj, mlp.fc, mlp.proj) on the last row of
+    each sequence, which is all that the head reads; then the last-row head.
+    The full last layer would add 2 (T - 1) (9 d^2 + d T) per sequence."""
     d, L, V = c["d_model"], c["n_layers"], c["vocab_size"]
-    return batch * (2.0 * T * L * 12 * d * d + 2.0 * L * d * T * (T + 1) + 2.0 * V * d)
+    full = 2.0 * T * (L - 1) * 12 * d * d + 2.0 * (L - 1) * d * T * (T + 1)
+    last = 2.0 * T * 3 * d * d + 2.0 * 9 * d * d + 4.0 * d * T
+    return batch * (full + last + 2.0 * V * d)
 
 
 def prompts_for(name: str, w: dict, vocab: int):

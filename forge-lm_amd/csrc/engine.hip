@@ -266,6 +266,7 @@ struct fh_session {
   FastDecode fast;
   bool fast_allowed = true;  // FORGE_HIP_FUSED_DECODE=0 at session creation selects the generic kernels
   bool bf16_act = true;      // FORGE_HIP_BF16_ACT=0 keeps a bf16 session's window GEMMs on fp32 operands
+  bool last_tail = true;     // FORGE_HIP_LAST_LAYER_TAIL=0 runs a window's last layer on every row
   bool counted = false;      // holds a reference on its context
   bool no_sampled_fused = false;  // set while fh_generate repeats a generation on the per-step path
   bool use_fast() const { return fast.enabled && fast_allowed; }
@@ -397,24 +398,62 @@ int head(fh_session* s, int B) {
   return FH_OK;
 }
 
+// Where the layers leave the last window row of each sequence (the head's input):
+// row r0 + b * stride of x.
+struct LastRows {
+  const float* x;
+  int stride, r0;
+};
+
 // bf16 sessions over many rows: the GEMM operands (LayerNorm, attention and GELU
 // outputs) are written in bf16, rounded as the fp32-operand GEMM rounds them, into
 // the same buffers (xn, o, h hold M*D, M*D, M*4D floats, twice the bf16 bytes).
 // The QKV GEMM writes q in bf16 (as the attention kernel rounds it) and K, V
 // straight into the bf16 caches.
-int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src) {
+//
+// After the window forward only the K/V caches and the last row of each sequence
+// are read (GptModel.ForwardLast takes the last row of the full forward,
+// src/LLM.Core/Models/GptModel.cs:202-209), so the last layer stops after its
+// qkv GEMM (which fills the caches) for all rows and runs the rest on the B last
+// rows only, as a batched decode step does: attention of the last query over the
+// window's keys, attn.proj, LN2, mlp.fc and mlp.proj on B rows.  The attention,
+// attn.proj, the MLP and LN2 of the other M - B rows of the last layer (9 d^2 +
+// 2 d t FLOP per row) are work whose result nothing reads.
+int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src, LastRows* last) {
   hipStream_t st = s->ctx->stream;
-  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T;
+  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T, L = s->d.n_layers;
   bf16_t* xnh = reinterpret_cast<bf16_t*>(s->xn);
   bf16_t* oh = reinterpret_cast<bf16_t*>(s->o);
   bf16_t* hh = reinterpret_cast<bf16_t*>(s->h);
   bf16_t* qh = reinterpret_cast<bf16_t*>(s->qkv);  // q [M][D] in bf16 (the fp32 qkv rows are not written)
-  for (int l = 0; l < s->d.n_layers; l++) {
+  // the last-row tail's fp32 rows in h (M * 4D floats, free once the last qkv GEMM ran):
+  // q [B][3D] (q columns only, the attention's qkv layout), x, x2, GELU [B][4D], y
+  const size_t BD = (size_t)B * D;
+  const bool tail = s->last_tail && 10 * BD <= (size_t)M * 4 * D;
+  for (int l = 0; l < L; l++) {
     bf16_t* kc = reinterpret_cast<bf16_t*>(s->kc) + (size_t)l * s->kv_layer;
     bf16_t* vc = reinterpret_cast<bf16_t*>(s->vc) + (size_t)l * s->kv_layer;
     LAUNCH(launch_layernorm_bf16(st, s->x, M, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), xnh, D, 1e-5f));
     LAUNCH(launch_gemm_bf16_qkv(st, xnh, M, D, s->wt<bf16_t>(s->idx_blk(l, 2)), s->v(s->idx_blk(l, 3)), src, T, H, C,
                                 qh, kc, vc));
+    if (tail && l + 1 == L) {
+      float* q1 = s->h;
+      float* x1 = q1 + 3 * BD;
+      float* x21 = x1 + BD;
+      float* f1 = x21 + BD;
+      float* y1 = f1 + 4 * BD;
+      LAUNCH(launch_gather_rows<bf16_t>(st, qh, D, T - 1, T, B, D, q1, 3 * D));
+      LAUNCH(launch_gather_rows<float>(st, s->x, D, T - 1, T, B, D, x1, D));
+      // the query at window position T - 1 over keys 0 .. T - 1
+      const RowSrc qsrc{src.tokens, src.step, src.tok_stride, src.tok_off + T - 1, T - 1, 0};
+      LAUNCH(launch_attn_decode_wide<bf16_t>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, s->o));
+      FH_TRY(linear<bf16_t>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, x1, x21));
+      LAUNCH(launch_layernorm(st, x21, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
+      FH_TRY(linear<bf16_t>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr, f1));
+      FH_TRY(linear<bf16_t>(s, f1, B, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, x21, y1));
+      *last = LastRows{y1, 1, 0};
+      break;
+    }
     LAUNCH(launch_attn_prefill_mfma_q16(st, qh, B, T, D, H, C, kc, vc, oh));
     LAUNCH(launch_gemm_bf16(st, oh, M, D, s->wt<bf16_t>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x,
                             s->x2, nullptr));
@@ -430,12 +469,13 @@ int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src) {
 }
 
 template <typename WT>
-int enqueue_layers_window(fh_session* s, int T, RowSrc src) {
+int enqueue_layers_window(fh_session* s, int T, RowSrc src, LastRows* last) {
   hipStream_t st = s->ctx->stream;
   const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T;
+  *last = LastRows{s->x, T, T - 1};
   if constexpr (sizeof(WT) == 2) {
     if (s->bf16_act && M >= 256 && D % 64 == 0 && D == 64 * H)
-      return enqueue_layers_window_bf16(s, T, src);
+      return enqueue_layers_window_bf16(s, T, src, last);
   }
   if (M > 4 && D % 32 == 0 && D <= 1024 && (size_t)M * 3 * D <= s->part_floats) {
     // short windows: the split-K reductions also store K/V and apply LN2 and the
@@ -629,9 +669,10 @@ int enqueue_window_step(fh_session* s, int T, const StepPlan& p) {
   RowSrc src{s->tokens, s->step, p.tok_stride, p.P - T, 0, 0};
   LAUNCH(launch_embed<WT>(st, src, B, T, s->w<WT>(s->idx_tok()), s->w<WT>(s->idx_pos()), D, s->d.vocab_size,
                           s->d.context_length, s->x));
-  FH_TRY(enqueue_layers_window<WT>(s, T, src));
+  LastRows last{};
+  FH_TRY(enqueue_layers_window<WT>(s, T, src, &last));
   const size_t lf = s->idx_lnf();
-  LAUNCH(launch_layernorm(st, s->x, B, 1, T, T - 1, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
+  LAUNCH(launch_layernorm(st, last.x, B, 1, last.stride, last.r0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
   FH_TRY(head<WT>(s, B));
   if (p.with_sample) LAUNCH(launch_sample(st, make_sample_args(s, p)));
   return FH_OK;
@@ -1134,6 +1175,8 @@ int fh_session_create(fh_context* c, const fh_model_desc* desc, fh_session** out
   sp->fast_allowed = !(fused_env && fused_env[0] == '0');
   const char* act_env = getenv("FORGE_HIP_BF16_ACT");
   sp->bf16_act = !(act_env && act_env[0] == '0');
+  const char* tail_env = getenv("FORGE_HIP_LAST_LAYER_TAIL");
+  sp->last_tail = !(tail_env && tail_env[0] == '0');
   if (sp->fast_allowed && (rc = sp->fast.init(*desc, c->props.multiProcessorCount)) != FH_OK)
     return fail(set_err(rc, "allocating the fused decode state failed"));
   c->sessions++;

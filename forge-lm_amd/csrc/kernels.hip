@@ -366,6 +366,16 @@ __global__ __launch_bounds__(256) void k_gemm_tiled(const float* __restrict__ A,
   }
 }
 
+// dst[r, c] = src[row0 + r * rstride, c] in fp32: one block per row.
+template <typename IT>
+__global__ __launch_bounds__(256) void k_gather_rows(const IT* __restrict__ src, int src_ld, int row0, int rstride,
+                                                     int d, float* __restrict__ dst, int dst_ld) {
+  const int r = blockIdx.x;
+  const IT* s = src + (size_t)(row0 + (size_t)r * rstride) * src_ld;
+  float* o = dst + (size_t)r * dst_ld;
+  for (int c = threadIdx.x; c < d; c += 256) o[c] = to_f32<IT>(s[c]);
+}
+
 // ---------------------------------------------------------------------------
 // KV cache store and attention
 // ---------------------------------------------------------------------------
@@ -1462,6 +1472,14 @@ hipError_t launch_gemm(hipStream_t st, const float* a, int M, int K, const WT* W
   return hipGetLastError();
 }
 
+template <typename IT>
+hipError_t launch_gather_rows(hipStream_t st, const IT* src, int src_ld, int row0, int rstride, int rows, int d,
+                              float* dst, int dst_ld) {
+  FH_CHECK_ARG(rows > 0 && d > 0 && src_ld >= d && dst_ld >= d && row0 >= 0 && rstride >= 0 && src && dst);
+  hipLaunchKernelGGL(k_gather_rows<IT>, dim3(rows), dim3(256), 0, st, src, src_ld, row0, rstride, d, dst, dst_ld);
+  return hipGetLastError();
+}
+
 template <typename KT>
 hipError_t launch_kv_store(hipStream_t st, RowSrc src, const float* qkv, int B, int T, int d, int H, int ctx,
                            KT* kcache, KT* vcache) {
@@ -1588,6 +1606,8 @@ template hipError_t launch_gemm<float>(hipStream_t, const float*, int, int, cons
                                        const float*, float*);
 template hipError_t launch_gemm<bf16_t>(hipStream_t, const float*, int, int, const bf16_t*, int, const float*, int,
                                         const float*, float*);
+template hipError_t launch_gather_rows<float>(hipStream_t, const float*, int, int, int, int, int, float*, int);
+template hipError_t launch_gather_rows<bf16_t>(hipStream_t, const bf16_t*, int, int, int, int, int, float*, int);
 template hipError_t launch_kv_store<float>(hipStream_t, RowSrc, const float*, int, int, int, int, int, float*,
                                            float*);
 template hipError_t launch_kv_store<bf16_t>(hipStream_t, RowSrc, const float*, int, int, int, int, int, bf16_t*,

@@ -49,6 +49,12 @@ template <typename WT>
 hipError_t launch_gemm(hipStream_t st, const float* a, int M, int K, const WT* W, int N, const float* bias, int epi,
                        const float* res, float* y);
 
+// dst[r, c] = src[row0 + r * rstride, c] (leading dimensions src_ld, dst_ld) in fp32,
+// for r < rows, c < d.
+template <typename IT>
+hipError_t launch_gather_rows(hipStream_t st, const IT* src, int src_ld, int row0, int rstride, int rows, int d,
+                              float* dst, int dst_ld);
+
 // K/V columns of qkv [B*T, 3d] into the cache [B][H][ctx][hd] at positions pos(row).
 template <typename KT>
 hipError_t launch_kv_store(hipStream_t st, RowSrc src, const float* qkv, int B, int T, int d, int H, int ctx,

@@ -619,6 +619,43 @@ def test_c5_shape_bf16_window_path_matches_oracle(fhp, oracle, backend, B, P):
                 assert ids[b][n] == int(np.argmax(ref)), (b, n)
 
 
+def test_bf16_window_last_layer_tail_matches_full_layer(fhp, oracle, backend):
+    # A bf16 window forward of 256 rows or more runs its last layer past the qkv GEMM
+    # (which fills the K/V caches for every row) on the last row of each sequence
+    # only; FORGE_HIP_LAST_LAYER_TAIL=0 at session creation runs it on every row.
+    # Both against the oracle on bf16-rounded parameters (2e-2) at every step: step 0
+    # is the window forward, steps 1..3 cached decode steps that read the caches the
+    # last layer's qkv GEMM wrote, and the two sessions against each other
+    shape = (4096, 128, 256, 3, 4)
+    B, P, NEW = 4, 64, 4
+    ocfg = oracle.Config(*shape)
+    w = oracle.trained_like(ocfg, oracle.init_weights(ocfg, 1234), 2234)
+    wr = bf16_round(w)[0]
+    prompts = np.stack([fhp.TrainingRandom(42 + b).ids(shape[0], P) for b in range(B)])
+    got = {}
+    for tail in ("1", "0"):
+        os.environ["FORGE_HIP_LAST_LAYER_TAIL"] = tail
+        try:
+            m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype="bf16")
+        finally:
+            del os.environ["FORGE_HIP_LAST_LAYER_TAIL"]
+        m.load_weights(w)
+        got[tail] = fhp.Sampler.generate(m, prompts, NEW, 0.0, 0, None, return_logits=True)
+        m.dispose()
+    (ids, lg), (ids0, lg0) = got["1"], got["0"]
+    for b in range(B):
+        assert rel_err(lg[b][0], lg0[b][0]) <= 2e-2, b
+        same = True  # the two sessions' windows agree until a near tie
+        for n in range(NEW):
+            window = np.concatenate([prompts[b], ids[b][:n]]).astype(np.int32)
+            ref = oracle.forward(ocfg, wr, window)[-1]
+            assert rel_err(lg[b][n], ref) <= 2e-2, (b, n)
+            top2 = np.sort(ref)[-2:]
+            same = same and top2[1] - top2[0] > 4e-2
+            if same:
+                assert ids[b][n] == int(np.argmax(ref)) == ids0[b][n], (b, n)
+
+
 @pytest.mark.parametrize("case", ["greedy_c2", "sampled", "slides", "eos"])
 def test_generate_stream_matches_one_shot(fhp, oracle, backend, case):
     # Sampler.Generate as an iterator: any chunking of fh_generate_next yields the ids
