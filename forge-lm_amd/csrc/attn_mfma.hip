@@ -39,22 +39,19 @@ __device__ __forceinline__ __bf16 to_bf(float f) { return __builtin_bit_cast(__b
 // grid dimension of nqb * H * B blocks; query block 0 holds the last BQ
 // queries (the most keys).  Workgroups reach the 8 XCDs round-robin by linear
 // index, so a grid ordered by query block gives one XCD every heaviest block.
-// When nqb is even and 8 divides H * B, XCD x takes whole (sequence, head)
-// groups (their K/V rows are fetched into its L2 once) as pairs of query
-// blocks i and nqb - 1 - i, whose costs add to the same total.  A block's
-// partner is the next index on its XCD, and the order within pairs flips every
-// 32 indices, so 4 blocks a CU receives, consecutive on the XCD or 32 apart,
-// form two whole pairs.  Otherwise the blocks keep the heaviest-first order.
+// When 8 divides H * B, XCD x takes whole (sequence, head) groups (their K/V
+// rows are fetched into its L2 only) and receives its blocks heaviest first:
+// query block 0 of each of its groups, then query block 1, and so on, so the
+// CUs that finish early pick up the light blocks at the end (longest job first).
+// Otherwise block L takes query block L mod nqb of group L / nqb.
 struct QBlock {
   int qb, h, b;
 };
 __device__ __forceinline__ QBlock prefill_block(int L, int nqb, int H) {
   const int G = gridDim.x / nqb;  // H * B
-  if ((nqb & 1) == 0 && G % 8 == 0) {
-    const int xcd = L & 7, s = L >> 3, j = s >> 1, half = nqb >> 1;
-    const int xh = j % half, g = xcd * (G / 8) + j / half;
-    const bool light = ((s + (s >> 5)) & 1) != 0;
-    return {light ? nqb - 1 - xh : xh, g % H, g / H};
+  if (G % 8 == 0) {
+    const int xcd = L & 7, s = L >> 3, gx = G / 8, g = xcd * gx + s % gx;
+    return {s / gx, g % H, g / H};
   }
   return {L % nqb, (L / nqb) % H, L / (nqb * H)};
 }
@@ -280,7 +277,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill_mfma(const QT* __restrict_
 // one FMA per score), the causal mask only on tiles that cross the wave's diagonal,
 // and P is rounded to bf16 by the hardware packed convert.  Rows at or past T
 // read as zeros (bounded buffer loads), so stale cache rows never meet a zero
-// weight.  Blocks take query blocks in prefill_block's XCD-balanced order.
+// weight.  Blocks take query blocks in prefill_block's order (heaviest first per XCD).
 // ---------------------------------------------------------------------------
 constexpr int KP = HD + 8;  // bf16 per LDS row of K (dims) and V^T (keys): 144 B, 16 rows hit distinct banks
 
