@@ -405,20 +405,53 @@ struct LastRows {
   int stride, r0;
 };
 
+// After a window forward only the K/V caches and the last row of each sequence
+// are read (GptModel.ForwardLast takes the last row of the full forward,
+// src/LLM.Core/Models/GptModel.cs:202-209), so the last layer stops after its qkv
+// projection and KV store (which fill the caches for every row) and runs the rest
+// on the B last rows only, as a batched decode step does: the attention of the
+// query at window position T - 1 over keys 0 .. T - 1, attn.proj, LN2, mlp.fc and
+// mlp.proj.  The attention, attn.proj, LN2 and MLP of the other B (T - 1) rows
+// (9 d^2 + 2 d t FLOP per row) are work whose result nothing reads.
+// FORGE_HIP_LAST_LAYER_TAIL=0 at session creation runs the layer on every row.
+bool last_rows_tail(const fh_session* s, int T) { return s->last_tail && T >= 3; }
+
+// q: layer l's q rows (row r at q + r * q_ld); x: the layer's input rows.  Uses h
+// (M * 4D floats, free once the last qkv projection ran) for the B-row operands:
+// q [B][3D] (q columns only, the attention's qkv layout), x, x2, GELU [B][4D], y.
+template <typename WT, typename QT>
+int enqueue_last_rows(fh_session* s, int T, RowSrc src, int l, const QT* q, int q_ld, LastRows* last) {
+  hipStream_t st = s->ctx->stream;
+  const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length;
+  const size_t BD = (size_t)B * D;
+  WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
+  WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
+  float* q1 = s->h;
+  float* x1 = q1 + 3 * BD;
+  float* x21 = x1 + BD;
+  float* f1 = x21 + BD;
+  float* y1 = f1 + 4 * BD;
+  LAUNCH(launch_gather_rows<QT>(st, q, q_ld, T - 1, T, B, D, q1, 3 * D));
+  LAUNCH(launch_gather_rows<float>(st, s->x, D, T - 1, T, B, D, x1, D));
+  const RowSrc qsrc{src.tokens, src.step, src.tok_stride, src.tok_off + T - 1, T - 1, 0};
+  if (D == 64 * H)
+    LAUNCH(launch_attn_decode_wide<WT>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, s->o));
+  else
+    LAUNCH(launch_attn_decode<WT>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, 64, s->o));
+  FH_TRY(linear<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, x1, x21));
+  LAUNCH(launch_layernorm(st, x21, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
+  FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr, f1));
+  FH_TRY(linear<WT>(s, f1, B, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, x21, y1));
+  *last = LastRows{y1, 1, 0};
+  return FH_OK;
+}
+
 // bf16 sessions over many rows: the GEMM operands (LayerNorm, attention and GELU
 // outputs) are written in bf16, rounded as the fp32-operand GEMM rounds them, into
 // the same buffers (xn, o, h hold M*D, M*D, M*4D floats, twice the bf16 bytes).
 // The QKV GEMM writes q in bf16 (as the attention kernel rounds it) and K, V
-// straight into the bf16 caches.
-//
-// After the window forward only the K/V caches and the last row of each sequence
-// are read (GptModel.ForwardLast takes the last row of the full forward,
-// src/LLM.Core/Models/GptModel.cs:202-209), so the last layer stops after its
-// qkv GEMM (which fills the caches) for all rows and runs the rest on the B last
-// rows only, as a batched decode step does: attention of the last query over the
-// window's keys, attn.proj, LN2, mlp.fc and mlp.proj on B rows.  The attention,
-// attn.proj, the MLP and LN2 of the other M - B rows of the last layer (9 d^2 +
-// 2 d t FLOP per row) are work whose result nothing reads.
+// straight into the bf16 caches.  The last layer ends on the last rows
+// (enqueue_last_rows).
 int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src, LastRows* last) {
   hipStream_t st = s->ctx->stream;
   const int B = s->B(), D = s->d.d_model, H = s->d.n_heads, C = s->d.context_length, M = B * T, L = s->d.n_layers;
@@ -426,34 +459,14 @@ int enqueue_layers_window_bf16(fh_session* s, int T, RowSrc src, LastRows* last)
   bf16_t* oh = reinterpret_cast<bf16_t*>(s->o);
   bf16_t* hh = reinterpret_cast<bf16_t*>(s->h);
   bf16_t* qh = reinterpret_cast<bf16_t*>(s->qkv);  // q [M][D] in bf16 (the fp32 qkv rows are not written)
-  // the last-row tail's fp32 rows in h (M * 4D floats, free once the last qkv GEMM ran):
-  // q [B][3D] (q columns only, the attention's qkv layout), x, x2, GELU [B][4D], y
-  const size_t BD = (size_t)B * D;
-  const bool tail = s->last_tail && 10 * BD <= (size_t)M * 4 * D;
+  const bool tail = last_rows_tail(s, T);
   for (int l = 0; l < L; l++) {
     bf16_t* kc = reinterpret_cast<bf16_t*>(s->kc) + (size_t)l * s->kv_layer;
     bf16_t* vc = reinterpret_cast<bf16_t*>(s->vc) + (size_t)l * s->kv_layer;
     LAUNCH(launch_layernorm_bf16(st, s->x, M, s->v(s->idx_blk(l, 0)), s->v(s->idx_blk(l, 1)), xnh, D, 1e-5f));
     LAUNCH(launch_gemm_bf16_qkv(st, xnh, M, D, s->wt<bf16_t>(s->idx_blk(l, 2)), s->v(s->idx_blk(l, 3)), src, T, H, C,
                                 qh, kc, vc));
-    if (tail && l + 1 == L) {
-      float* q1 = s->h;
-      float* x1 = q1 + 3 * BD;
-      float* x21 = x1 + BD;
-      float* f1 = x21 + BD;
-      float* y1 = f1 + 4 * BD;
-      LAUNCH(launch_gather_rows<bf16_t>(st, qh, D, T - 1, T, B, D, q1, 3 * D));
-      LAUNCH(launch_gather_rows<float>(st, s->x, D, T - 1, T, B, D, x1, D));
-      // the query at window position T - 1 over keys 0 .. T - 1
-      const RowSrc qsrc{src.tokens, src.step, src.tok_stride, src.tok_off + T - 1, T - 1, 0};
-      LAUNCH(launch_attn_decode_wide<bf16_t>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, s->o));
-      FH_TRY(linear<bf16_t>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, x1, x21));
-      LAUNCH(launch_layernorm(st, x21, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
-      FH_TRY(linear<bf16_t>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr, f1));
-      FH_TRY(linear<bf16_t>(s, f1, B, 4 * D, s->idx_blk(l, 10), D, s->v(s->idx_blk(l, 11)), EPI_RESIDUAL, x21, y1));
-      *last = LastRows{y1, 1, 0};
-      break;
-    }
+    if (tail && l + 1 == L) return enqueue_last_rows<bf16_t, bf16_t>(s, T, src, l, qh, D, last);
     LAUNCH(launch_attn_prefill_mfma_q16(st, qh, B, T, D, H, C, kc, vc, oh));
     LAUNCH(launch_gemm_bf16(st, oh, M, D, s->wt<bf16_t>(s->idx_blk(l, 4)), D, s->v(s->idx_blk(l, 5)), EPI_NONE, s->x,
                             s->x2, nullptr));
@@ -482,6 +495,7 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src, LastRows* last) {
     // next layer's LN1, as in batched decode (the last mlp.proj keeps its residual
     // epilogue: LN_f runs on the last rows only)
     const int L = s->d.n_layers;
+    const bool tail = last_rows_tail(s, T);
     LAUNCH(launch_layernorm(st, s->x, M, M, 0, 0, s->v(s->idx_blk(0, 0)), s->v(s->idx_blk(0, 1)), s->xn, D, 1e-5f));
     for (int l = 0; l < L; l++) {
       WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
@@ -489,6 +503,7 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src, LastRows* last) {
       int S = 0;
       FH_TRY(linear_parts<WT>(s, s->xn, M, D, s->idx_blk(l, 2), 3 * D, &S));
       LAUNCH(launch_epilogue_qkv<WT>(st, s->part, S, M, D, s->v(s->idx_blk(l, 3)), s->qkv, src, T, H, C, kc, vc));
+      if (tail && l + 1 == L) return enqueue_last_rows<WT, float>(s, T, src, l, s->qkv, 3 * D, last);
       if (D == 64 * H)
         LAUNCH((launch_attn_prefill_mfma<WT, float>(st, s->qkv, B, T, D, H, C, kc, vc, s->o)));
       else
@@ -509,6 +524,7 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src, LastRows* last) {
     }
     return FH_OK;
   }
+  const bool tail = last_rows_tail(s, T);
   for (int l = 0; l < s->d.n_layers; l++) {
     WT* kc = reinterpret_cast<WT*>(s->kc) + (size_t)l * s->kv_layer;
     WT* vc = reinterpret_cast<WT*>(s->vc) + (size_t)l * s->kv_layer;
@@ -516,6 +532,7 @@ int enqueue_layers_window(fh_session* s, int T, RowSrc src, LastRows* last) {
     FH_TRY(linear<WT>(s, s->xn, M, D, s->idx_blk(l, 2), 3 * D, s->v(s->idx_blk(l, 3)), EPI_NONE, nullptr,
                       s->qkv));
     LAUNCH(launch_kv_store<WT>(st, src, s->qkv, B, T, D, H, C, kc, vc));
+    if (tail && l + 1 == s->d.n_layers) return enqueue_last_rows<WT, float>(s, T, src, l, s->qkv, 3 * D, last);
     if (D == 64 * H)
       LAUNCH((launch_attn_prefill_mfma<WT, float>(st, s->qkv, B, T, D, H, C, kc, vc, s->o)));
     else
