@@ -399,7 +399,7 @@ int head(fh_session* s, int B) {
 }
 
 // Where the layers leave the last window row of each sequence (the head's input):
-// row r0 + b * stride of x.
+// row r0 + b * stride of x; x == nullptr: LN_f of those rows is already in xn.
 struct LastRows {
   const float* x;
   int stride, r0;
@@ -438,6 +438,21 @@ int enqueue_last_rows(fh_session* s, int T, RowSrc src, int l, const QT* q, int 
     LAUNCH(launch_attn_decode_wide<WT>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, s->o));
   else
     LAUNCH(launch_attn_decode<WT>(st, qsrc, q1, B, D, H, C, kc, vc, s->apart, 64, s->o));
+  if (decode_fused_epilogues(s)) {
+    // as in batched decode: the split-K sums of attn.proj and mlp.proj fused with
+    // the LayerNorm after them (LN2, LN_f), so xn holds the head's input on return
+    int S = 0;
+    const size_t lf = s->idx_lnf();
+    FH_TRY(linear_parts<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, &S));
+    LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 5)), x1, x21, s->v(s->idx_blk(l, 6)),
+                              s->v(s->idx_blk(l, 7)), s->xn, 1e-5f));
+    FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr, f1));
+    FH_TRY(linear_parts<WT>(s, f1, B, 4 * D, s->idx_blk(l, 10), D, &S));
+    LAUNCH(launch_epilogue_ln(st, s->part, S, B, D, s->v(s->idx_blk(l, 11)), x21, y1, s->v(lf), s->v(lf + 1), s->xn,
+                              1e-5f));
+    *last = LastRows{nullptr, 0, 0};
+    return FH_OK;
+  }
   FH_TRY(linear<WT>(s, s->o, B, D, s->idx_blk(l, 4), D, s->v(s->idx_blk(l, 5)), EPI_NONE, x1, x21));
   LAUNCH(launch_layernorm(st, x21, B, B, 0, 0, s->v(s->idx_blk(l, 6)), s->v(s->idx_blk(l, 7)), s->xn, D, 1e-5f));
   FH_TRY(linear<WT>(s, s->xn, B, D, s->idx_blk(l, 8), 4 * D, s->v(s->idx_blk(l, 9)), EPI_GELU, nullptr, f1));
@@ -689,7 +704,8 @@ int enqueue_window_step(fh_session* s, int T, const StepPlan& p) {
   LastRows last{};
   FH_TRY(enqueue_layers_window<WT>(s, T, src, &last));
   const size_t lf = s->idx_lnf();
-  LAUNCH(launch_layernorm(st, last.x, B, 1, last.stride, last.r0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
+  if (last.x)
+    LAUNCH(launch_layernorm(st, last.x, B, 1, last.stride, last.r0, s->v(lf), s->v(lf + 1), s->xn, D, 1e-5f));
   FH_TRY(head<WT>(s, B));
   if (p.with_sample) LAUNCH(launch_sample(st, make_sample_args(s, p)));
   return FH_OK;
