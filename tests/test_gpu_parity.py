@@ -1115,3 +1115,56 @@ def test_in_kernel_sampler_ties_repeat_the_generation_per_step(fhp, oracle, back
     ids = fhp.Sampler.generate(m, prompt, 30, 0.9, 20, fhp.Random(8), repetition_penalty=1.3, return_logits=True)[0]
     np.testing.assert_array_equal(fused, ids)
     m.dispose()
+
+
+@pytest.mark.parametrize("path", ["fused_greedy", "fused_sampled", "batched_fp32", "window_bf16"])
+def test_each_path_gives_the_same_bits_run_to_run(fhp, oracle, backend, path):
+    """Same inputs, same bits (the reference's same-seed determinism,
+    tests/LLM.Core.Tests/ModelTests.cs:45-56): every reduction on the device runs in a
+    fixed order (DPP trees, split-K partials summed in split order, the two K halves
+    of a bf16 tile added as ((own + other) + bias) + residual whichever half arrives
+    first, the fused step's hand-offs gathered by slot), so two runs on one session and
+    a run on a second session with the same weights return the same ids and, where
+    the path returns them, the same logits bit for bit.  Paths: the persistent batch-1
+    kernel (greedy, and sampled with top-k, penalty and n-gram bans), the batched fp32
+    decode graph (attention combined in attn.proj's operand load) and bf16 windows of
+    8 x 1024 rows (every step re-prefills; mlp.proj with its K split in two)."""
+    N = fhp._native
+    if path in ("fused_greedy", "fused_sampled"):
+        shape, B, P, NEW, dtype = (16384, 1024, 768, 2, 12), 1, 40, 200, "f32"
+        want = N.FH_ROUTE_FUSED_STEP | (N.FH_ROUTE_FUSED_SAMPLER if path == "fused_sampled" else 0)
+    elif path == "batched_fp32":
+        shape, B, P, NEW, dtype = (16384, 1024, 768, 2, 12), 8, 300, 16, "f32"
+        want = N.FH_ROUTE_ATTN_IN_PROJ
+    else:
+        shape, B, P, NEW, dtype = (16384, 1024, 1024, 2, 16), 8, 1024, 2, "bf16"
+        want = 0
+    ocfg = oracle.Config(*shape)
+    w = oracle.trained_like(ocfg, oracle.init_weights(ocfg, 77), 1077)
+    r = fhp.TrainingRandom(5)
+    prompts = np.stack([r.ids(shape[0], P) for _ in range(B)])
+    if B == 1:
+        prompts = prompts[0]
+
+    def run(model):
+        if path == "fused_sampled":
+            return fhp.Sampler.generate(model, prompts, NEW, 0.7, 30, fhp.Random(9), repetition_penalty=1.1,
+                                        no_repeat_ngram_size=4), None
+        if path == "fused_greedy":
+            return fhp.Sampler.generate(model, prompts, NEW, 0.0, 0, None), None
+        return fhp.Sampler.generate(model, prompts, NEW, 0.0, 0, None, return_logits=True)
+
+    models = []
+    for _ in range(2):
+        m = fhp.GptModel(fhp.ModelConfig(*shape), backend, batch=B, dtype=dtype)
+        m.load_weights(w)
+        models.append(m)
+    first = run(models[0])
+    assert route(fhp) & want == want, (path, route(fhp))
+    for again in (run(models[0]), run(models[1])):
+        np.testing.assert_array_equal(again[0], first[0])
+        if first[1] is not None:
+            assert np.array_equal(np.asarray(again[1], np.float32).view(np.uint32),
+                                  np.asarray(first[1], np.float32).view(np.uint32)), path
+    for m in models:
+        m.dispose()
