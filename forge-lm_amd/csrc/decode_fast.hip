@@ -578,9 +578,12 @@ struct SampLds<true> {
 // between steps, so they are read from HBM once per launch instead of once per
 // token; 12 fill the LDS the sampled kernel leaves); INFLIGHT of the rest stream
 // from HBM at a time.  Both are measured per kernel: the greedy kernel holds 4
-// and streams three at a time (145.7 against 147.5 us per token holding none; 6,
-// 8 or 12 rows measured 152.7-156.7: the layers' code came out slower), the
-// sampled kernel holds 12 and streams two at a time.
+// and streams two at a time (145.7 against 147.5 us per token holding none; 6,
+// 8 or 12 rows measured 152.7-156.7: the layers' code came out slower; later, with
+// the current tile request sites, 2, 3, 5, 6 or 8 rows 141.9-144.0 against 136.6,
+// and one, two or three rows in flight 138.2 / 135.7-136.1 / 136.5-136.7), the
+// sampled kernel holds 12 and streams two at a time (one or three: 152.7 / 150.4
+// against 149.9).
 #ifndef FH_HRES_G
 #define FH_HRES_G 4
 #endif
@@ -588,7 +591,7 @@ struct SampLds<true> {
 #define FH_HRES_S 12
 #endif
 #ifndef FH_HG_G
-#define FH_HG_G 3
+#define FH_HG_G 2
 #endif
 #ifndef FH_HG_S
 #define FH_HG_S 2
